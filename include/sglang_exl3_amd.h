@@ -1,0 +1,109 @@
+/*
+ * sglang_exl3_amd — C ABI of the MI355X (gfx950) EXL3 quantized-matmul path.
+ *
+ * Plain pointers, sizes and a HIP stream (passed as void*; NULL = the null
+ * stream).  Every device pointer must point into memory of the current HIP
+ * device.  Every entry point returns EXL3_OK (0) or a non-zero status, and
+ * exl3_last_error() then describes the failure (thread-local string).
+ * Kernels are enqueued asynchronously on `stream`; no entry point
+ * synchronises, allocates device memory or copies to the host, so all of them
+ * can be captured into a HIP graph.
+ *
+ * Element types: "f16" = IEEE binary16 bits (uint16_t), "f32" = float,
+ * trellis words = int16 as stored by EXL3 ([k/16][n/16][16*K] row-major).
+ * Codebook ids follow the reference: 0 = 3INST, 1 = MCG, 2 = mul1.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the reference repository).
+ */
+#ifndef SGLANG_EXL3_AMD_H
+#define SGLANG_EXL3_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_ABI_VERSION 1
+
+#define EXL3_OK 0
+#define EXL3_ERR_ARG 1         /* bad shape, size, pointer or parameter */
+#define EXL3_ERR_UNSUPPORTED 2 /* valid input outside the implemented set */
+#define EXL3_ERR_HIP 3         /* HIP runtime / launch failure */
+#define EXL3_ERR_WORKSPACE 4   /* workspace missing or too small */
+
+#define EXL3_CB_3INST 0
+#define EXL3_CB_MCG 1
+#define EXL3_CB_MUL1 2
+
+/* Version of this ABI (EXL3_ABI_VERSION).  Replaces the pybind module
+ * attribute P2B_MOE_ABI_VERSION (csrc/bindings.cpp:170). */
+int exl3_abi_version(void);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* exl3_last_error(void);
+
+/* Decode a whole EXL3 weight to fp16, bit-identical to the reference host
+ * dequant (truncating codebook rounding, two fp32 FWHT passes, RNE store).
+ * W: f16 [k][n].  K in 1..8, k and n multiples of 128.
+ * Replaces dequant_trellis (csrc/bindings.cpp:117-132; torch op
+ * sglang_exl3::dequant_trellis, src/sglang_exl3/ops.py:38-54). */
+int exl3_dequant_trellis(const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+                         uint16_t* W, int k, int n, int K, int codebook, void* stream);
+
+/* Decode `count` raw 16-bit trellis states with a codebook: out[i] = f16 bits
+ * of the codebook entry, rounded toward zero (round_toward_zero != 0, the
+ * host reference's rounding) or to nearest-even (0, the CUDA kernels' one).
+ * Device twin of decode_codebook_bits (csrc/exl3_dequant.cuh:74-93) and
+ * decode_3inst (csrc/quant/codebook.cuh:56-90). */
+int exl3_decode_states(const uint16_t* states, int count, int codebook, int round_toward_zero,
+                       uint16_t* out, void* stream);
+
+/* Decode every 16x16 tile of a trellis into W (f16 [k][n]) without the
+ * Hadamard rotations or sign scales: W[16kt+r][16nt+c] = value of tile
+ * (kt,nt) at row r, column c.  The per-tile part of dequant_cpu
+ * (csrc/bindings.cpp:37-76). */
+int exl3_decode_tiles(const int16_t* trellis, uint16_t* W, int k, int n, int K, int codebook,
+                      int round_toward_zero, void* stream);
+
+/* Scratch bytes exl3_gemv / exl3_gemm / exl3_p2b_gemv_batched need for a
+ * problem of `experts` independent GEMVs of [m,k]x[k,n].  The workspace must
+ * be zero-filled before its first use; every call leaves it zero-filled again
+ * (its counters self-reset).  Concurrent calls must use distinct workspaces. */
+size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int experts);
+
+/* y[m][n] (f16) = x[m][k] (f16) . W, W = the EXL3 weight (suh, trellis, svh).
+ * Input rotation, decode, fp32-accumulated MFMA product and output rotation
+ * run in one launch.  m in 1..64.
+ * Replaces exl3_gemv (csrc/bindings.cpp:134-147 -> csrc/exl3_gemv.cu:23-63;
+ * torch op sglang_exl3::exl3_gemv, src/sglang_exl3/ops.py:57-74). */
+int exl3_gemv(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+              uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/* Same product for any number of rows m >= 1 (prefill).
+ * Replaces exl3_gemm (csrc/bindings.cpp:110-115 -> csrc/exl3_gemm.cu:9-31;
+ * torch op sglang_exl3::exl3_gemm, src/sglang_exl3/ops.py:77-93). */
+int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+              uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/* For each active slot e < num_active: out[e] (f16 [m][n]) = x_e . W_{ids[e]}
+ * where x_e = x (x_per_expert == 0, x is [m][k]) or x + e*m*k (x_per_expert
+ * != 0, x is [num_active][m][k]); weight pointers come from int64 device
+ * tables indexed by ids (int32).  One launch for all slots.
+ * Replaces p2b_gemv_batched (csrc/bindings.cpp:149-156 ->
+ * csrc/p2b_batched.cu:78-101; torch op sglang_exl3::p2b_gemv_batched,
+ * src/sglang_exl3/ops.py:96-118). */
+int exl3_p2b_gemv_batched(const uint16_t* x, int x_per_expert, const int64_t* trellis_ptrs,
+                          const int64_t* suh_ptrs, const int64_t* svh_ptrs, const int32_t* ids,
+                          int num_active, uint16_t* out, int m, int k, int n, int K, int codebook,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGLANG_EXL3_AMD_H */

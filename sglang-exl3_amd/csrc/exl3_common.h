@@ -1,0 +1,54 @@
+// Shared host-side helpers of the C ABI: error reporting and launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/sglang_exl3_amd.h"
+
+namespace exl3 {
+
+// Thread-local message behind exl3_last_error().
+void set_error(const char* fmt, ...);
+void clear_error();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Check the launch just enqueued; converts a HIP error into EXL3_ERR_HIP.
+inline int launch_status(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: %s", what, hipGetErrorString(e));
+        return EXL3_ERR_HIP;
+    }
+    return EXL3_OK;
+}
+
+// Workspace layout shared by every split-k kernel: a fixed region of int
+// counters first (zero between calls; each call's last workgroups reset the
+// ones they used), then the fp32 partial sums.  The fixed offset keeps one
+// call's partials from ever overlapping another shape's counters.
+constexpr size_t kWsCounterBytes = 256 * 1024;
+constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int);
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace exl3
+
+#define EXL3_REQUIRE(cond, ...)                  \
+    do {                                         \
+        if (!(cond)) {                           \
+            exl3::set_error(__VA_ARGS__);        \
+            return EXL3_ERR_ARG;                 \
+        }                                        \
+    } while (0)
+
+#define EXL3_REQUIRE_CODE(cond, code, ...)       \
+    do {                                         \
+        if (!(cond)) {                           \
+            exl3::set_error(__VA_ARGS__);        \
+            return (code);                       \
+        }                                        \
+    } while (0)

@@ -1,0 +1,155 @@
+// EXL3 trellis decode primitives for CDNA4 (gfx950).
+//
+// Format (the reference's, restated): a 16x16 weight tile is a tail-biting
+// bitstream of 256*K bits held as 8*K little-endian uint32 words.  Value t of
+// the tile is the 16-bit window ending at stream bit (t+1)*K, bits taken
+// MSB-first across words (csrc/exl3_dequant.cuh:110-135,
+// csrc/quant/exl3_dq.cuh:15-30).  Value t lands at
+//   k = 2(l%4) + (j&1) + 8((j>>1)&1),  n = l/4 + 8(j>>2),  l = t/8, j = t%8
+// inside the tile (csrc/bindings.cpp:51-75).
+//
+// Work split used by every kernel here: one lane owns a "32-state group"
+// q = 0..7 of a tile, i.e. the tile's values [32q, 32q+32).  Their windows end
+// at bits 32Kq + (u+1)K, u = 0..31, so the group needs exactly the K words
+// [Kq, Kq+K) plus the word before them (the tile's last word for q = 0).
+// Those 32 values are columns q and q+8 of the tile, each with all 16 k rows:
+//   run h = 0 (u = 0..15)  -> k in {0,1,8,9,2,3,10,11} + 0
+//   run h = 1 (u = 16..31) -> k in {0,1,8,9,2,3,10,11} + 4
+// for column q from u%16 in {0,1,2,3,8,9,10,11} and for column q+8 from
+// u%16 in {4,5,6,7,12,13,14,15}.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kHadNorm = 0.08838834764831845f;  // 1/sqrt(128)
+
+// k offsets (inside a 16-row tile) of the 8 values one run gives one column,
+// in decode order; the second run adds 4.
+__host__ __device__ constexpr int kofs(int e) {
+    return e == 0 ? 0 : e == 1 ? 1 : e == 2 ? 8 : e == 3 ? 9 : e == 4 ? 2 : e == 5 ? 3 : e == 6 ? 10 : 11;
+}
+
+// ------------------------------------------------------------------ windows
+
+// 16-bit window of local value u (0..31) from the lane's word buffer
+// buf[0] = previous word, buf[1..K] = own words.  Shifts are compile-time.
+template <int K, int U>
+__device__ __forceinline__ uint32_t window(const uint32_t* buf) {
+    constexpr int rel_end = 32 + (U + 1) * K;
+    constexpr int rel_start = rel_end - 16;
+    constexpr int ia = rel_start / 32;
+    constexpr int ib = (rel_end - 1) / 32;
+    constexpr int sh = 32 * (ib + 1) - rel_end;
+    if constexpr (ia == ib) {
+        return __builtin_amdgcn_ubfe(buf[ib], sh, 16);
+    } else {
+        return __builtin_amdgcn_alignbit(buf[ia], buf[ib], sh) & 0xffffu;
+    }
+}
+
+// ---------------------------------------------------------------- codebooks
+
+// x = state * M (+ 64248484 for 3INST) mod 2^32.  v_mul_lo_u32 issues at the
+// full VALU rate on gfx950 (measured: same throughput as v_fma_f32).
+template <int CB>
+__device__ __forceinline__ uint32_t hash(uint32_t s) {
+    constexpr uint32_t M = CB == 0 ? 89226354u : CB == 1 ? 0xCBAC1FEDu : 0x83DCD12Du;
+    uint32_t x = s * M;
+    if constexpr (CB == 0) x += 64248484u;
+    return x;
+}
+
+__device__ __forceinline__ uint32_t cb_mask(uint32_t x) { return (x & 0x8fff8fffu) ^ 0x3b603b60u; }
+
+// Round-to-nearest decode of two states into a packed half2 (the rounding of
+// the reference's CUDA kernels, csrc/quant/codebook.cuh:41,53,65,74,88).
+template <int CB>
+__device__ __forceinline__ uint32_t decode2_rn(uint32_t s0, uint32_t s1) {
+    uint32_t x0 = hash<CB>(s0), x1 = hash<CB>(s1);
+    if constexpr (CB == 2) {
+        uint32_t h0 = __builtin_amdgcn_udot4(x0, 0x01010101u, 0x6400u, false);
+        uint32_t h1 = __builtin_amdgcn_udot4(x1, 0x01010101u, 0x6400u, false);
+        uint32_t p = __builtin_amdgcn_perm(h1, h0, 0x05040100u);
+        __half2 hp = *reinterpret_cast<__half2*>(&p);
+        const __half2 kinv = __halves2half2(__ushort_as_half(0x1eee), __ushort_as_half(0x1eee));
+        const __half2 bias = __halves2half2(__ushort_as_half(0xc931), __ushort_as_half(0xc931));
+        __half2 r = __hfma2(hp, kinv, bias);
+        return *reinterpret_cast<uint32_t*>(&r);
+    } else {
+        uint32_t y0 = cb_mask(x0), y1 = cb_mask(x1);
+        __half2 a = *reinterpret_cast<__half2*>(&y0);
+        __half2 b = *reinterpret_cast<__half2*>(&y1);
+        __half v0 = __hadd(__low2half(a), __high2half(a));
+        __half v1 = __hadd(__low2half(b), __high2half(b));
+        __half2 r = __halves2half2(v0, v1);
+        return *reinterpret_cast<uint32_t*>(&r);
+    }
+}
+
+// Exact fp32 value of a codebook entry (every intermediate is exact).
+template <int CB>
+__device__ __forceinline__ float decode_exact(uint32_t s) {
+    uint32_t x = hash<CB>(s);
+    if constexpr (CB == 2) {
+        uint32_t h = __builtin_amdgcn_udot4(x, 0x01010101u, 0x6400u, false);
+        // h * 0x1eee + 0xc931: 0x1eee = 1774 * 2^-18, 0xc931 = -2721792 * 2^-18;
+        // the product and the sum are exact in fp32.
+        float hf = __half2float(__ushort_as_half((unsigned short)h));
+        return hf * (1774.0f / 262144.0f) + (-2721792.0f / 262144.0f);
+    } else {
+        uint32_t y = cb_mask(x);
+        return __half2float(__ushort_as_half((unsigned short)(y & 0xffffu))) +
+               __half2float(__ushort_as_half((unsigned short)(y >> 16)));
+    }
+}
+
+// Truncating decode of two states (the reference's host dequant rounding,
+// csrc/exl3_dequant.cuh:41-55): exact fp32 value, then fp16 round-toward-zero.
+template <int CB>
+__device__ __forceinline__ uint32_t decode2_rz(uint32_t s0, uint32_t s1) {
+    float a = decode_exact<CB>(s0), b = decode_exact<CB>(s1);
+    auto r = __builtin_amdgcn_cvt_pkrtz(a, b);
+    return *reinterpret_cast<uint32_t*>(&r);
+}
+
+// ------------------------------------------------------------- group decode
+
+// Fragment element e (0..7) of column half c and run h comes from local value
+// u = 16h + (e & 3) + 8(e >> 2) + 4c and sits at tile row k = 4h + kofs(e).
+template <int K, int CB, bool RZ, int H, int C, int P>
+__device__ __forceinline__ uint32_t frag_pair(const uint32_t* buf) {
+    constexpr int e0 = 2 * P, e1 = 2 * P + 1;
+    constexpr int u0 = 16 * H + (e0 & 3) + 8 * (e0 >> 2) + 4 * C;
+    constexpr int u1 = 16 * H + (e1 & 3) + 8 * (e1 >> 2) + 4 * C;
+    uint32_t s0 = window<K, u0>(buf), s1 = window<K, u1>(buf);
+    if constexpr (RZ) return decode2_rz<CB>(s0, s1);
+    else return decode2_rn<CB>(s0, s1);
+}
+
+template <int K, int CB, bool RZ, int H, int C>
+__device__ __forceinline__ void frag_decode(const uint32_t* buf, uint32_t* f) {
+    f[0] = frag_pair<K, CB, RZ, H, C, 0>(buf);
+    f[1] = frag_pair<K, CB, RZ, H, C, 1>(buf);
+    f[2] = frag_pair<K, CB, RZ, H, C, 2>(buf);
+    f[3] = frag_pair<K, CB, RZ, H, C, 3>(buf);
+}
+
+// Decode the 32 values of one lane's group into the four MFMA B fragments
+// frag[c][h] (8 halves each): column q + 8c, k rows of run h.
+template <int K, int CB, bool RZ>
+__device__ __forceinline__ void decode_group(const uint32_t* buf, uint32_t frag[2][2][4]) {
+    frag_decode<K, CB, RZ, 0, 0>(buf, frag[0][0]);
+    frag_decode<K, CB, RZ, 1, 0>(buf, frag[0][1]);
+    frag_decode<K, CB, RZ, 0, 1>(buf, frag[1][0]);
+    frag_decode<K, CB, RZ, 1, 1>(buf, frag[1][1]);
+}
+
+}  // namespace exl3

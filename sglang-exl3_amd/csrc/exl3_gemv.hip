@@ -1,0 +1,193 @@
+// C ABI of the GEMV family (exl3_gemv, exl3_gemm's skinny path,
+// exl3_p2b_gemv_batched) and the gfx950 launch-shape selector that replaces
+// the reference's per-architecture tables (csrc/exl3_gemv.cu:10-21, 40-48;
+// csrc/quant/exl3_kernel_map.cuh:53-62).
+#include <stdlib.h>
+
+#include "exl3_gemv_impl.h"
+
+namespace exl3 {
+
+int gemv_launch_K1(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K2(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K3(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K4(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K5(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K6(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K7(int, int, const GemvParams&, int, hipStream_t);
+int gemv_launch_K8(int, int, const GemvParams&, int, hipStream_t);
+
+int gemv_launch(int K, int cb, int mb, const GemvParams& p, int experts, hipStream_t st) {
+    switch (K) {
+        case 1: return gemv_launch_K1(cb, mb, p, experts, st);
+        case 2: return gemv_launch_K2(cb, mb, p, experts, st);
+        case 3: return gemv_launch_K3(cb, mb, p, experts, st);
+        case 4: return gemv_launch_K4(cb, mb, p, experts, st);
+        case 5: return gemv_launch_K5(cb, mb, p, experts, st);
+        case 6: return gemv_launch_K6(cb, mb, p, experts, st);
+        case 7: return gemv_launch_K7(cb, mb, p, experts, st);
+        case 8: return gemv_launch_K8(cb, mb, p, experts, st);
+    }
+    set_error("exl3 gemv: K=%d outside 1..8", K);
+    return EXL3_ERR_UNSUPPORTED;
+}
+
+namespace {
+
+constexpr int kMaxGemvRows = 64;
+constexpr size_t kMaxGemvSmem = 64 * 1024;
+
+struct GemvPlan {
+    int mb;
+    int kts;
+    int splits;
+};
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+// gfx950 launch shape: every workgroup covers a 128-column block (one output
+// FWHT block) and `kts` k-slices.  The split count is the smallest that
+// still gives at least `target` workgroups (256 CUs, a few resident each),
+// so per-workgroup fixed costs (input rotation, reduction) stay small.
+GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
+    GemvPlan pl;
+    pl.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    const int kslices = k / 16;
+    const int max_kts = 4 * (K <= 4 ? 8 : 4);
+    const long long target = env_int("EXL3_GEMV_TARGET_WGS", 1024);
+    const int forced = env_int("EXL3_GEMV_KTS", 0);
+    const long long cols = (long long)(n / 128) * experts;
+    int best = 8;
+    for (int kts = 8; kts <= max_kts && kts <= kslices; kts += 8) {
+        if (kslices % kts) continue;
+        if (gemv_smem_bytes(m, kts) > kMaxGemvSmem) continue;
+        if (forced > 0) {
+            if (kts == forced) best = kts;
+            continue;
+        }
+        if (cols * (kslices / kts) >= target || kts == 8) best = kts;
+    }
+    pl.kts = best;
+    pl.splits = kslices / best;
+    return pl;
+}
+
+size_t workspace_bytes_for(const GemvPlan& pl, int m, int n, int experts) {
+    if (pl.splits <= 1) return 0;
+    const size_t nblk = (size_t)(n / 128) * experts;
+    return kWsCounterBytes + nblk * pl.splits * (size_t)m * 128 * sizeof(float);
+}
+
+int check_common(const char* fn, int m, int k, int n, int K, int codebook) {
+    EXL3_REQUIRE(m >= 1, "%s: m=%d must be >= 1", fn, m);
+    EXL3_REQUIRE(k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0,
+                 "%s: k=%d n=%d must be positive multiples of 128", fn, k, n);
+    EXL3_REQUIRE(K >= 1 && K <= 8, "%s: K=%d outside 1..8", fn, K);
+    EXL3_REQUIRE(codebook >= 0 && codebook <= 2, "%s: codebook=%d outside 0..2", fn, codebook);
+    return EXL3_OK;
+}
+
+int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, void* ws, size_t ws_bytes,
+             hipStream_t st) {
+    GemvPlan pl = plan_gemv(p.m, p.k, p.n, K, experts);
+    const size_t need = workspace_bytes_for(pl, p.m, p.n, experts);
+    EXL3_REQUIRE_CODE(need == 0 || (ws && ws_bytes >= need), EXL3_ERR_WORKSPACE,
+                      "%s: workspace of %zu bytes needed, %zu given", fn, need, ws ? ws_bytes : (size_t)0);
+    p.kts = pl.kts;
+    p.splits = pl.splits;
+    if (need) {
+        EXL3_REQUIRE_CODE((size_t)(p.n / 128) * experts <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
+                          "%s: %d column blocks exceed the %zu workspace counters", fn, (p.n / 128) * experts,
+                          kWsMaxCounters);
+        p.counters = reinterpret_cast<int*>(ws);
+        p.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsCounterBytes);
+    } else {
+        p.counters = nullptr;
+        p.partials = nullptr;
+    }
+    return gemv_launch(K, codebook, pl.mb, p, experts, st);
+}
+
+GemvParams base_params(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+                       uint16_t* y, int m, int k, int n) {
+    GemvParams p{};
+    p.x = reinterpret_cast<const __half*>(x);
+    p.trellis = reinterpret_cast<const uint32_t*>(trellis);
+    p.suh = reinterpret_cast<const __half*>(suh);
+    p.svh = reinterpret_cast<const __half*>(svh);
+    p.y = reinterpret_cast<__half*>(y);
+    p.m = m;
+    p.k = k;
+    p.n = n;
+    return p;
+}
+
+}  // namespace
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int experts) {
+    if (m < 1 || k < 128 || n < 128 || experts < 1) return 0;
+    const int mc = m > kMaxGemvRows ? kMaxGemvRows : m;
+    GemvPlan pl = plan_gemv(mc, k, n, K, experts);
+    return workspace_bytes_for(pl, mc, n, experts);
+}
+
+extern "C" int exl3_gemv(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+                         uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_common("exl3_gemv", m, k, n, K, codebook);
+    if (rc) return rc;
+    EXL3_REQUIRE(m <= kMaxGemvRows, "exl3_gemv: m=%d above %d (use exl3_gemm)", m, kMaxGemvRows);
+    EXL3_REQUIRE(x && trellis && suh && svh && y, "exl3_gemv: null pointer");
+    EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4) && aligned(svh, 4) && aligned(trellis, 16),
+                 "exl3_gemv: misaligned pointer");
+    GemvParams p = base_params(x, trellis, suh, svh, y, m, k, n);
+    return run_gemv("exl3_gemv", p, K, codebook, 1, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+                         uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_common("exl3_gemm", m, k, n, K, codebook);
+    if (rc) return rc;
+    EXL3_REQUIRE(x && trellis && suh && svh && y, "exl3_gemm: null pointer");
+    EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4) && aligned(svh, 4) && aligned(trellis, 16),
+                 "exl3_gemm: misaligned pointer");
+    hipStream_t st = as_stream(stream);
+    for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
+        const int mc = (m - r0) < kMaxGemvRows ? (m - r0) : kMaxGemvRows;
+        GemvParams p = base_params(x + (size_t)r0 * k, trellis, suh, svh, y + (size_t)r0 * n, mc, k, n);
+        rc = run_gemv("exl3_gemm", p, K, codebook, 1, workspace, workspace_bytes, st);
+        if (rc) return rc;
+    }
+    return EXL3_OK;
+}
+
+extern "C" int exl3_p2b_gemv_batched(const uint16_t* x, int x_per_expert, const int64_t* trellis_ptrs,
+                                     const int64_t* suh_ptrs, const int64_t* svh_ptrs, const int32_t* ids,
+                                     int num_active, uint16_t* out, int m, int k, int n, int K, int codebook,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_common("exl3_p2b_gemv_batched", m, k, n, K, codebook);
+    if (rc) return rc;
+    EXL3_REQUIRE(m <= kMaxGemvRows, "exl3_p2b_gemv_batched: m=%d above %d", m, kMaxGemvRows);
+    EXL3_REQUIRE(num_active >= 1 && num_active <= 65535, "exl3_p2b_gemv_batched: num_active=%d", num_active);
+    EXL3_REQUIRE(x && trellis_ptrs && suh_ptrs && svh_ptrs && ids && out, "exl3_p2b_gemv_batched: null pointer");
+    GemvParams p = base_params(x, nullptr, nullptr, nullptr, out, m, k, n);
+    p.t_tab = trellis_ptrs;
+    p.su_tab = suh_ptrs;
+    p.sv_tab = svh_ptrs;
+    p.ids = ids;
+    p.x_stride_e = x_per_expert ? (long long)m * k : 0;
+    p.y_stride_e = (long long)m * n;
+    return run_gemv("exl3_p2b_gemv_batched", p, K, codebook, num_active, workspace, workspace_bytes,
+                    as_stream(stream));
+}

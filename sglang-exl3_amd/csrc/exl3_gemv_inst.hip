@@ -1,0 +1,16 @@
+// One instantiation unit of the GEMV kernels per bit width: the build
+// compiles this file once per K with -DEXL3_K=K (keeps compile units small).
+#include "exl3_gemv_impl.h"
+
+#ifndef EXL3_K
+#error "build with -DEXL3_K=<bits>"
+#endif
+
+#define EXL3_CAT2(a, b) a##b
+#define EXL3_CAT(a, b) EXL3_CAT2(a, b)
+
+namespace exl3 {
+int EXL3_CAT(gemv_launch_K, EXL3_K)(int cb, int mb, const GemvParams& p, int experts, hipStream_t st) {
+    return gemv_launch_k<EXL3_K>(cb, mb, p, experts, st);
+}
+}  // namespace exl3

@@ -1,0 +1,273 @@
+"""torch.library custom ops ``torch.ops.sglang_exl3.*`` backed by the gfx950 HIP library.
+
+Same op names, schemas, mutation annotations and fake (meta) kernels as the
+reference registry (src/sglang_exl3/ops.py:29-230), so SGLang's graph runner,
+piecewise graphs and torch.compile see the same surface.  Every op enqueues
+its kernels on the current HIP stream of the input's device through the C
+ABI (include/sglang_exl3_amd.h); non-zero statuses become RuntimeError.
+CPU tensors are rejected: there is no CPU fallback in the product.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Dict, Tuple
+
+import torch
+
+from . import _lib
+
+logger = logging.getLogger("sglang.exl3.ops")
+
+_OPS_REGISTERED = False
+
+# Reference op list (tests/test_cuda_graph.py:15-23)
+OP_NAMES = (
+    "dequant_trellis",
+    "exl3_gemv",
+    "exl3_gemm",
+    "p2b_gemv_batched",
+    "p2b_fused_moe",
+    "exl3_fat_gemm",
+    "exl3_fat_gemm_scatter",
+)
+
+# ---------------------------------------------------------------- plumbing
+
+_WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _stream_ptr(t: torch.Tensor) -> int:
+    return int(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_device(name: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(f"sglang_exl3::{name} requires HIP device tensors (got {t.device})")
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"sglang_exl3::{name}: tensors on different devices ({dev}, {t.device})")
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-initialised scratch keyed by (device, current stream).  Kernels
+    leave their counters zero after each call, so the buffer is reused as is;
+    growth allocates a new zeroed buffer (stream-ordered, like the reference's
+    per-stream workspace in src/sglang_exl3/dense.py:45-58)."""
+    key = (device.index or 0, int(torch.cuda.current_stream(device).cuda_stream))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 20, 0 if ws is None else 2 * ws.numel())
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def _check_trellis(name: str, trellis: torch.Tensor, K: int) -> None:
+    if trellis.dim() != 3 or trellis.dtype != torch.int16:
+        raise RuntimeError(f"sglang_exl3::{name}: trellis must be int16 [k/16, n/16, 16*K]")
+    if int(trellis.shape[2]) != 16 * int(K):
+        raise RuntimeError(
+            f"sglang_exl3::{name}: trellis last dim {int(trellis.shape[2])} != 16*K ({16 * int(K)})"
+        )
+
+
+def _f16(name: str, t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.float16:
+        raise RuntimeError(f"sglang_exl3::{name}: {what} must be float16 (got {t.dtype})")
+    return t.contiguous()
+
+
+# ------------------------------------------------------------ implementations
+
+def dequant_trellis_impl(trellis, suh, svh, bits, mcg):
+    _require_device("dequant_trellis", trellis, suh, svh)
+    _check_trellis("dequant_trellis", trellis, bits)
+    k, n = int(trellis.shape[0]) * 16, int(trellis.shape[1]) * 16
+    suh = _f16("dequant_trellis", suh, "suh")
+    svh = _f16("dequant_trellis", svh, "svh")
+    if suh.numel() < k or svh.numel() < n:
+        raise RuntimeError("sglang_exl3::dequant_trellis: suh/svh are too short")
+    tr = trellis.contiguous()
+    W = torch.empty((k, n), dtype=torch.float16, device=trellis.device)
+    with torch.cuda.device(trellis.device):
+        rc = _lib.lib().exl3_dequant_trellis(
+            tr.data_ptr(), suh.data_ptr(), svh.data_ptr(), W.data_ptr(), k, n, int(bits),
+            _lib.codebook_from_mcg(bool(mcg)), _stream_ptr(trellis))
+    _lib.check(rc, "exl3_dequant_trellis")
+    return W
+
+
+def _gemv_like(name, fn, x, trellis, suh, svh, K, mcg, max_rows=None):
+    _require_device(name, x, trellis, suh, svh)
+    _check_trellis(name, trellis, K)
+    if x.dim() < 2:
+        raise RuntimeError(f"sglang_exl3::{name}: x must have shape [..., in_features]")
+    kdim = int(x.shape[-1])
+    m = x.numel() // kdim if kdim else 0
+    if kdim != int(trellis.shape[0]) * 16:
+        raise RuntimeError(f"sglang_exl3::{name}: x feature dimension does not match trellis")
+    if max_rows is not None and not (1 <= m <= max_rows):
+        raise RuntimeError(f"sglang_exl3::{name}: native GEMV supports 1 <= m <= {max_rows} (m={m})")
+    x2 = _f16(name, x, "x").reshape(m, kdim)
+    n = int(trellis.shape[1]) * 16
+    suh = _f16(name, suh, "suh")
+    svh = _f16(name, svh, "svh")
+    tr = trellis.contiguous()
+    y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    lib = _lib.lib()
+    with torch.cuda.device(x.device):
+        need = int(lib.exl3_gemv_workspace_size(min(m, 64), kdim, n, int(K), 1))
+        ws = workspace(x.device, need) if need else None
+        rc = fn(x2.data_ptr(), tr.data_ptr(), suh.data_ptr(), svh.data_ptr(), y.data_ptr(), m, kdim, n,
+                int(K), _lib.codebook_from_mcg(bool(mcg)), 0 if ws is None else ws.data_ptr(),
+                0 if ws is None else ws.numel(), _stream_ptr(x))
+    _lib.check(rc, name)
+    return y
+
+
+def exl3_gemv_impl(x, trellis, suh, svh, K, mcg, mmode=1):
+    if mmode not in (0, 1):
+        raise RuntimeError("sglang_exl3::exl3_gemv: mmode must be 0 or 1")
+    return _gemv_like("exl3_gemv", _lib.lib().exl3_gemv, x, trellis, suh, svh, K, mcg, max_rows=64)
+
+
+def exl3_gemm_impl(x, trellis, suh, svh, K, mcg):
+    return _gemv_like("exl3_gemm", _lib.lib().exl3_gemm, x, trellis, suh, svh, K, mcg)
+
+
+def p2b_gemv_batched_impl(x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices, K, mcg, mmode=1):
+    name = "p2b_gemv_batched"
+    _require_device(name, x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices)
+    x = _f16(name, x, "x")
+    for t, what in ((trellis_ptrs, "trellis_ptrs"), (suh_ptrs, "suh_ptrs"), (svh_ptrs, "svh_ptrs")):
+        if t.dtype != torch.int64 or t.dim() != 1:
+            raise RuntimeError(f"sglang_exl3::{name}: {what} must be a 1-D int64 pointer table")
+    ids = expert_indices.to(torch.int32).contiguous()
+    e = ids.numel()
+    kdim = int(x.shape[-1])
+    per_expert = x.dim() == 3
+    m = int(x.shape[1]) if per_expert else int(x.shape[0])
+    if per_expert and int(x.shape[0]) != e:
+        raise RuntimeError(f"sglang_exl3::{name}: 3-D x must be [num_active, m, k]")
+    n = int(mmode) if int(mmode) > 0 else 2048
+    out = torch.empty((e, m, n), dtype=torch.float16, device=x.device)
+    if e == 0:
+        return out
+    lib = _lib.lib()
+    with torch.cuda.device(x.device):
+        need = int(lib.exl3_gemv_workspace_size(m, kdim, n, int(K), e))
+        ws = workspace(x.device, need) if need else None
+        rc = lib.exl3_p2b_gemv_batched(
+            x.data_ptr(), int(per_expert), trellis_ptrs.contiguous().data_ptr(),
+            suh_ptrs.contiguous().data_ptr(), svh_ptrs.contiguous().data_ptr(), ids.data_ptr(), e,
+            out.data_ptr(), m, kdim, n, int(K), _lib.codebook_from_mcg(bool(mcg)),
+            0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream_ptr(x))
+    _lib.check(rc, name)
+    return out
+
+
+def _not_built(name):
+    def _fn(*args, **kwargs):
+        raise RuntimeError(f"sglang_exl3::{name} is not implemented in this build")
+    return _fn
+
+
+p2b_fused_moe_impl = _not_built("p2b_fused_moe")
+exl3_fat_gemm_impl = _not_built("exl3_fat_gemm")
+exl3_fat_gemm_scatter_impl = _not_built("exl3_fat_gemm_scatter")
+
+
+# ----------------------------------------------------------------- registry
+
+def register_custom_ops() -> bool:
+    """Register the EXL3 kernels in torch.ops.sglang_exl3 with fake kernels
+    (same schemas as src/sglang_exl3/ops.py:38-226)."""
+    global _OPS_REGISTERED
+    if _OPS_REGISTERED:
+        return True
+
+    @torch.library.custom_op("sglang_exl3::dequant_trellis", mutates_args=())
+    def dequant_trellis(trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, bits: int,
+                        mcg: bool) -> torch.Tensor:
+        return dequant_trellis_impl(trellis, suh, svh, bits, mcg)
+
+    @dequant_trellis.register_fake
+    def _(trellis, suh, svh, bits, mcg):
+        return torch.empty((trellis.size(0) * 16, trellis.size(1) * 16), dtype=torch.float16,
+                           device=trellis.device)
+
+    @torch.library.custom_op("sglang_exl3::exl3_gemv", mutates_args=())
+    def exl3_gemv(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
+                  mcg: bool, mmode: int = 1) -> torch.Tensor:
+        return exl3_gemv_impl(x, trellis, suh, svh, K, mcg, mmode)
+
+    @exl3_gemv.register_fake
+    def _(x, trellis, suh, svh, K, mcg, mmode=1):
+        out_dim = svh.size(0) if svh.ndim == 1 else trellis.size(1) * 16
+        return torch.empty((x.shape[0], out_dim), dtype=x.dtype, device=x.device)
+
+    @torch.library.custom_op("sglang_exl3::exl3_gemm", mutates_args=())
+    def exl3_gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
+                  mcg: bool) -> torch.Tensor:
+        return exl3_gemm_impl(x, trellis, suh, svh, K, mcg)
+
+    @exl3_gemm.register_fake
+    def _(x, trellis, suh, svh, K, mcg):
+        out_dim = svh.size(0) if svh.ndim == 1 else trellis.size(1) * 16
+        return torch.empty((x.shape[0], out_dim), dtype=x.dtype, device=x.device)
+
+    @torch.library.custom_op("sglang_exl3::p2b_gemv_batched", mutates_args=())
+    def p2b_gemv_batched(x: torch.Tensor, trellis_ptrs: torch.Tensor, suh_ptrs: torch.Tensor,
+                         svh_ptrs: torch.Tensor, expert_indices: torch.Tensor, K: int, mcg: bool,
+                         mmode: int = 1) -> torch.Tensor:
+        return p2b_gemv_batched_impl(x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices, K, mcg, mmode)
+
+    @p2b_gemv_batched.register_fake
+    def _(x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices, K, mcg, mmode=1):
+        e = expert_indices.numel()
+        m = x.size(1) if x.dim() == 3 else x.size(0)
+        n = mmode if mmode > 0 else 2048
+        return torch.empty((e, m, n), dtype=x.dtype, device=x.device)
+
+    @torch.library.custom_op("sglang_exl3::p2b_fused_moe", mutates_args=("out",))
+    def p2b_fused_moe(x: torch.Tensor, out: torch.Tensor, gate_trellis_ptrs: torch.Tensor,
+                      gate_suh_ptrs: torch.Tensor, gate_svh_ptrs: torch.Tensor, up_trellis_ptrs: torch.Tensor,
+                      up_suh_ptrs: torch.Tensor, up_svh_ptrs: torch.Tensor, down_trellis_ptrs: torch.Tensor,
+                      down_suh_ptrs: torch.Tensor, down_svh_ptrs: torch.Tensor, expert_indices: torch.Tensor,
+                      routing_weights: torch.Tensor, K_gate: int, K_up: int, K_down: int,
+                      mcg: bool) -> None:
+        p2b_fused_moe_impl(x, out, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs,
+                           up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs,
+                           expert_indices, routing_weights, K_gate, K_up, K_down, mcg)
+
+    @p2b_fused_moe.register_fake
+    def _(x, out, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs,
+          down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs, expert_indices, routing_weights, K_gate, K_up,
+          K_down, mcg):
+        return None
+
+    @torch.library.custom_op("sglang_exl3::exl3_fat_gemm", mutates_args=("out",))
+    def exl3_fat_gemm(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor, K: int,
+                      mcg: bool, mul1: bool) -> None:
+        exl3_fat_gemm_impl(a, packed, out, svh, K, mcg, mul1)
+
+    @exl3_fat_gemm.register_fake
+    def _(a, packed, out, svh, K, mcg, mul1):
+        return None
+
+    @torch.library.custom_op("sglang_exl3::exl3_fat_gemm_scatter", mutates_args=("out",))
+    def exl3_fat_gemm_scatter(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor,
+                              token_idx: torch.Tensor, route_weight: torch.Tensor, K: int, mcg: bool,
+                              mul1: bool) -> None:
+        exl3_fat_gemm_scatter_impl(a, packed, out, svh, token_idx, route_weight, K, mcg, mul1)
+
+    @exl3_fat_gemm_scatter.register_fake
+    def _(a, packed, out, svh, token_idx, route_weight, K, mcg, mul1):
+        return None
+
+    _OPS_REGISTERED = True
+    logger.info("registered sglang_exl3 custom ops (gfx950 HIP backend)")
+    return True

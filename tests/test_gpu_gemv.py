@@ -1,0 +1,158 @@
+"""GPU parity of exl3_gemv / exl3_gemm / p2b_gemv_batched against the CPU oracle.
+
+Bar: max-abs-err <= 2e-2 * rms(ref) and cosine >= 0.9999
+against x @ dequant(W) accumulated in fp32 or better.  The dequantised W is the
+oracle's (bit-exact restatement of the reference host dequant); at the full
+BASELINE sizes the GPU dequant (pinned bit-exact in test_gpu_decode.py) stands in
+for it, with a block spot-checked against the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import check_close, make_weight, make_x, to_dev
+from sglang_exl3 import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _registered():
+    ops.register_custom_ops()
+
+
+def _oracle_ref(x, trellis, suh, svh, K, cb):
+    W = oracle.dequant(trellis, suh, svh, K, cb, rtz=True)
+    return oracle.matmul(x, W)
+
+
+@pytest.mark.parametrize("m,k,n,K,cb", [
+    (1, 256, 256, 4, 1), (1, 512, 384, 3, 1), (2, 256, 512, 2, 1), (3, 384, 256, 4, 2),
+    (8, 512, 256, 5, 1), (8, 256, 256, 3, 2), (4, 256, 256, 4, 0), (16, 256, 384, 4, 1),
+    (17, 256, 256, 3, 1), (33, 256, 256, 4, 2), (64, 256, 256, 2, 1), (1, 256, 256, 1, 1),
+    (2, 256, 256, 6, 2), (1, 256, 256, 7, 1), (5, 256, 256, 8, 1),
+])
+def test_gemv_small_vs_oracle(m, k, n, K, cb):
+    print(f"case: gemv m={m} k={k} n={n} K={K} cb={cb}", flush=True)
+    trellis, suh, svh = make_weight(k, n, K, seed=1000 + 17 * K + cb + m)
+    x = make_x(m, k, seed=m * 31 + K)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    if cb == 0:
+        y = _run_capi(xd, tr, su, sv, K, cb)
+    else:
+        y = torch.ops.sglang_exl3.exl3_gemv(xd, tr, su, sv, K, cb == 1, 1)
+    torch.cuda.synchronize()
+    assert y.shape == (m, n) and y.dtype == torch.float16
+    ref = _oracle_ref(x, trellis, suh, svh, K, cb)
+    check_close(y.float().cpu().numpy(), ref, f"gemv m={m} K={K} cb={cb}")
+
+
+def _run_capi(xd, tr, su, sv, K, cb):
+    m, k = xd.shape
+    n = tr.shape[1] * 16
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    L = _lib.lib()
+    need = int(L.exl3_gemv_workspace_size(m, k, n, K, 1))
+    ws = ops.workspace(xd.device, need) if need else None
+    rc = L.exl3_gemv(xd.data_ptr(), tr.data_ptr(), su.data_ptr(), sv.data_ptr(), y.data_ptr(), m, k, n, K, cb,
+                     0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+                     int(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, "exl3_gemv")
+    return y
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_gemv_baseline_config2_full_size(m):
+    """k=4096, n=14336, K=4, MCG, seeded random trellis, +-1 signs."""
+    print(f"case: gemv cfg2 full size m={m}", flush=True)
+    k, n, K = 4096, 14336, 4
+    trellis, suh, svh = make_weight(k, n, K, seed=2)
+    x = make_x(m, k, seed=20 + m)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    W = torch.ops.sglang_exl3.dequant_trellis(tr, su, sv, K, True)
+    # spot-check one 128x128 block of the GPU dequant against the oracle
+    blk = oracle.dequant(trellis[8:16, 40:48], suh[128:256], svh[640:768], K, 1, rtz=True)
+    assert np.array_equal(W[128:256, 640:768].cpu().numpy().view(np.uint16), blk)
+    ref = (xd.float() @ W.float()).cpu().numpy()
+    y = torch.ops.sglang_exl3.exl3_gemv(xd, tr, su, sv, K, True, 1)
+    check_close(y.float().cpu().numpy(), ref, f"cfg2 m={m}")
+
+
+def test_gemv_deterministic():
+    k, n, K = 2048, 4096, 3
+    trellis, suh, svh = make_weight(k, n, K, seed=5)
+    x = make_x(4, k, seed=5)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    y1 = torch.ops.sglang_exl3.exl3_gemv(xd, tr, su, sv, K, True, 1)
+    y2 = torch.ops.sglang_exl3.exl3_gemv(xd, tr, su, sv, K, True, 1)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+def test_gemv_zero_trellis_closed_form():
+    """All-zero trellis (the reference's own fixture, tests/test_cuda_graph.py:76-78): only
+    output columns 128j are non-zero, y[:,128j] = 128 c svh[128j] sum_i x[:,128i] suh[128i]."""
+    k, n = 512, 384
+    for mcg, c in ((True, 1.84375), (False, -3.453125)):
+        rng = np.random.default_rng(11)
+        x = rng.standard_normal((2, k)).astype(np.float16)
+        suh = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+        svh = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+        tr = torch.zeros((k // 16, n // 16, 32), dtype=torch.int16, device="cuda")
+        xd, su, sv = to_dev(x, suh, svh)
+        y = torch.ops.sglang_exl3.exl3_gemv(xd, tr, su, sv, 2, mcg, 1).float().cpu().numpy()
+        s = (x.astype(np.float64)[:, ::128] * suh.astype(np.float64)[::128]).sum(axis=1)
+        want = 128.0 * c * s[:, None] * svh.astype(np.float64)[None, ::128]
+        assert np.allclose(y[:, ::128], want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+        mask = np.ones(n, dtype=bool)
+        mask[::128] = False
+        assert np.abs(y[:, mask]).max() <= 1e-3 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("m", [1, 16, 64, 130])
+def test_gemm_any_rows(m):
+    print(f"case: gemm m={m}", flush=True)
+    k, n, K = 512, 256, 3
+    trellis, suh, svh = make_weight(k, n, K, seed=40 + m)
+    x = make_x(m, k, seed=41 + m)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    y = torch.ops.sglang_exl3.exl3_gemm(xd, tr, su, sv, K, False)
+    ref = _oracle_ref(x, trellis, suh, svh, K, 2)
+    check_close(y.float().cpu().numpy(), ref, f"gemm m={m}")
+
+
+@pytest.mark.parametrize("per_expert", [False, True])
+def test_p2b_gemv_batched(per_expert):
+    print(f"case: p2b_gemv_batched per_expert={per_expert}", flush=True)
+    E, k, n, K, m = 6, 256, 384, 3, 2
+    ws = [make_weight(k, n, K, seed=300 + e) for e in range(E)]
+    dev = [to_dev(*w) for w in ws]
+    tptr = torch.tensor([d[0].data_ptr() for d in dev], dtype=torch.int64, device="cuda")
+    uptr = torch.tensor([d[1].data_ptr() for d in dev], dtype=torch.int64, device="cuda")
+    vptr = torch.tensor([d[2].data_ptr() for d in dev], dtype=torch.int64, device="cuda")
+    ids = [4, 0, 5, 4]
+    idt = torch.tensor(ids, dtype=torch.int32, device="cuda")
+    if per_expert:
+        x = np.stack([make_x(m, k, seed=500 + j) for j in range(len(ids))])
+    else:
+        x = make_x(m, k, seed=500)
+    (xd,) = to_dev(x)
+    out = torch.ops.sglang_exl3.p2b_gemv_batched(xd, tptr, uptr, vptr, idt, K, True, n)
+    assert out.shape == (len(ids), m, n)
+    for j, e in enumerate(ids):
+        xe = x[j] if per_expert else x
+        ref = _oracle_ref(xe, *ws[e], K, 1)
+        check_close(out[j].float().cpu().numpy(), ref, f"batched slot {j} expert {e}")
+
+
+def test_gemv_rejects_bad_shapes():
+    trellis, suh, svh = make_weight(256, 256, 4, seed=1)
+    x = make_x(1, 256, seed=1)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    with pytest.raises(RuntimeError):
+        torch.ops.sglang_exl3.exl3_gemv(xd, tr, su, sv, 3, True, 1)  # K does not match trellis
+    with pytest.raises(RuntimeError):
+        torch.ops.sglang_exl3.exl3_gemv(xd[:, :128].contiguous(), tr, su, sv, 4, True, 1)
+    with pytest.raises(RuntimeError):
+        torch.ops.sglang_exl3.exl3_gemv(xd.cpu(), tr, su, sv, 4, True, 1)
