@@ -74,6 +74,13 @@ int exl3_decode_tiles(const int16_t* trellis, uint16_t* W, int k, int n, int K, 
  * (its counters self-reset).  Concurrent calls must use distinct workspaces. */
 size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int experts);
 
+/* Launch shape the gfx950 selector picks for a GEMV problem:
+ * out[0] = 16-row blocks, out[1] = steps (4 k-slices) per wave,
+ * out[2] = k waves per workgroup, out[3] = k-splits across workgroups,
+ * out[4] = LDS bytes per workgroup.  Replaces the per-architecture kernel
+ * tables (csrc/exl3_gemv.cu:10-21, 40-48; csrc/quant/exl3_kernel_map.cuh:53-62). */
+int exl3_gemv_plan(int m, int k, int n, int K, int experts, int* out);
+
 /* y[m][n] (f16) = x[m][k] (f16) . W, W = the EXL3 weight (suh, trellis, svh).
  * Input rotation, decode, fp32-accumulated MFMA product and output rotation
  * run in one launch.  m in 1..64.

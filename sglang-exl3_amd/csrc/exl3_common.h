@@ -33,6 +33,14 @@ inline int launch_status(const char* what) {
 constexpr size_t kWsCounterBytes = 256 * 1024;
 constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int);
 
+// LDS a gfx950 workgroup may allocate.
+constexpr size_t kMaxLds = 160 * 1024;
+
+// Let `kernel` take up to `need` bytes of dynamic LDS (the runtime default cap
+// is 64 KB).  Checks the device limit and the kernel's static LDS; returns
+// EXL3_OK or an error with a message.
+int allow_dynamic_lds(const void* kernel, size_t need, const char* what);
+
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 }  // namespace exl3

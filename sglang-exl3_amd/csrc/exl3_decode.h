@@ -23,6 +23,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace exl3 {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -30,6 +32,16 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kHadNorm = 0.08838834764831845f;  // 1/sqrt(128)
+
+// Global-address-space view of a pointer.  Pointers read from tables or
+// selected at run time are generic to the compiler, which then emits FLAT
+// loads; those count against the LDS counter too, so every LDS wait would
+// also wait for all outstanding HBM loads.  Global loads keep them apart.
+#define EXL3_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ EXL3_GLOBAL T* gptr(T* p) {
+    return (EXL3_GLOBAL T*)p;
+}
 
 // k offsets (inside a 16-row tile) of the 8 values one run gives one column,
 // in decode order; the second run adds 4.
@@ -69,14 +81,20 @@ __device__ __forceinline__ uint32_t hash(uint32_t s) {
 
 __device__ __forceinline__ uint32_t cb_mask(uint32_t x) { return (x & 0x8fff8fffu) ^ 0x3b603b60u; }
 
+// Sum of the four bytes of x plus acc (the mul1 codebook's byte sum), as one
+// v_sad_u8 (sum of |byte - 0|).  v_sad_u8 is a plain VALU op: the dot-product
+// form (v_dot4_u32_u8) fed straight into an MFMA operand gave wrong products
+// on gfx950 (its result was consumed by the MFMA one instruction later).
+__device__ __forceinline__ uint32_t byte_sum(uint32_t x, uint32_t acc) { return __builtin_amdgcn_sad_u8(x, 0u, acc); }
+
 // Round-to-nearest decode of two states into a packed half2 (the rounding of
 // the reference's CUDA kernels, csrc/quant/codebook.cuh:41,53,65,74,88).
 template <int CB>
 __device__ __forceinline__ uint32_t decode2_rn(uint32_t s0, uint32_t s1) {
     uint32_t x0 = hash<CB>(s0), x1 = hash<CB>(s1);
     if constexpr (CB == 2) {
-        uint32_t h0 = __builtin_amdgcn_udot4(x0, 0x01010101u, 0x6400u, false);
-        uint32_t h1 = __builtin_amdgcn_udot4(x1, 0x01010101u, 0x6400u, false);
+        uint32_t h0 = byte_sum(x0, 0x6400u);
+        uint32_t h1 = byte_sum(x1, 0x6400u);
         uint32_t p = __builtin_amdgcn_perm(h1, h0, 0x05040100u);
         __half2 hp = *reinterpret_cast<__half2*>(&p);
         const __half2 kinv = __halves2half2(__ushort_as_half(0x1eee), __ushort_as_half(0x1eee));
@@ -99,7 +117,7 @@ template <int CB>
 __device__ __forceinline__ float decode_exact(uint32_t s) {
     uint32_t x = hash<CB>(s);
     if constexpr (CB == 2) {
-        uint32_t h = __builtin_amdgcn_udot4(x, 0x01010101u, 0x6400u, false);
+        uint32_t h = byte_sum(x, 0x6400u);
         // h * 0x1eee + 0xc931: 0x1eee = 1774 * 2^-18, 0xc931 = -2721792 * 2^-18;
         // the product and the sum are exact in fp32.
         float hf = __half2float(__ushort_as_half((unsigned short)h));
@@ -122,8 +140,51 @@ __device__ __forceinline__ uint32_t decode2_rz(uint32_t s0, uint32_t s1) {
 
 // ------------------------------------------------------------- group decode
 
-// Fragment element e (0..7) of column half c and run h comes from local value
-// u = 16h + (e & 3) + 8(e >> 2) + 4c and sits at tile row k = 4h + kofs(e).
+// Matmul-side decode ("pair form"): one 32-bit word per value, holding two
+// fp16 numbers whose contribution to the product is their sum times x:
+//   3INST / MCG: the two masked halves (lo, hi) — value = lo + hi, exactly the
+//                pre-rounding sum the codebook adds (codebook.cuh:56-75);
+//   mul1:        (h, -1534) with h = 1024 + byte_sum — value = kinv*h + bias
+//                = kinv*(h - 1534) + delta, so the product is accumulated on
+//                (h - 1534) and scaled by kinv (+ delta * sum(x)) afterwards
+//                (codebook.cuh:76-89).
+// The matmul pairs each word with the activation duplicated in both halves, so
+// no fp16 add / fma is spent per value and the MFMA accumulates exactly in fp32.
+constexpr uint32_t kMul1PairBias = 0xE5FE6400u;  // high half: fp16(-1534); low half: 0x6400
+constexpr float kMul1Kinv = 1774.0f / 262144.0f;  // fp16 0x1eee
+// delta = bias + 1534 * kinv = (-2721792 + 1534 * 1774) * 2^-18
+constexpr float kMul1Delta = (float)(-2721792 + 1534 * 1774) / 262144.0f;
+
+template <int CB>
+__device__ __forceinline__ uint32_t decode_pair_word(uint32_t s) {
+    const uint32_t x = hash<CB>(s);
+    if constexpr (CB == 2) return byte_sum(x, kMul1PairBias);
+    else return cb_mask(x);
+}
+
+template <int K, int CB, int U>
+__device__ __forceinline__ void pair_one(const uint32_t* buf, uint32_t* out) {
+    out[U] = decode_pair_word<CB>(window<K, U>(buf));
+}
+
+template <int K, int CB, int... Us>
+__device__ __forceinline__ void pair_all(const uint32_t* buf, uint32_t* out, std::integer_sequence<int, Us...>) {
+    (pair_one<K, CB, Us>(buf, out), ...);
+}
+
+// All 32 values of a lane's group in pair form, in value order u = 0..31.
+// Writing u = 8Q + 4c + t (Q = 0..3, c = 0..1, t = 0..3): value u is column
+// q + 8c of the tile at row k = 4(Q >> 1) + kofs(4(Q & 1) + t), so each run
+// of four consecutive values is one MFMA B fragment (one column, 4 rows).
+template <int K, int CB>
+__device__ __forceinline__ void decode_group_pairs(const uint32_t* buf, uint32_t out[32]) {
+    pair_all<K, CB>(buf, out, std::make_integer_sequence<int, 32>{});
+}
+
+// Tile row of value slot t (0..3) of quarter Q (0..3).
+__host__ __device__ constexpr int quarter_row(int Q, int t) { return 4 * (Q >> 1) + kofs(4 * (Q & 1) + t); }
+
+// Exact-rounding decode (dequant / decode ops): fp16 bits of two values.
 template <int K, int CB, bool RZ, int H, int C, int P>
 __device__ __forceinline__ uint32_t frag_pair(const uint32_t* buf) {
     constexpr int e0 = 2 * P, e1 = 2 * P + 1;
@@ -142,8 +203,8 @@ __device__ __forceinline__ void frag_decode(const uint32_t* buf, uint32_t* f) {
     f[3] = frag_pair<K, CB, RZ, H, C, 3>(buf);
 }
 
-// Decode the 32 values of one lane's group into the four MFMA B fragments
-// frag[c][h] (8 halves each): column q + 8c, k rows of run h.
+// Decode the 32 values of one lane's group into fp16 words frag[c][h][p]
+// (values 2p, 2p+1 of column q + 8c, run h; tile row 4h + kofs(e)).
 template <int K, int CB, bool RZ>
 __device__ __forceinline__ void decode_group(const uint32_t* buf, uint32_t frag[2][2][4]) {
     frag_decode<K, CB, RZ, 0, 0>(buf, frag[0][0]);

@@ -35,12 +35,13 @@ int gemv_launch(int K, int cb, int mb, const GemvParams& p, int experts, hipStre
 namespace {
 
 constexpr int kMaxGemvRows = 64;
-constexpr size_t kMaxGemvSmem = 64 * 1024;
+constexpr size_t kMaxGemvSmem = kMaxLds;
 
 struct GemvPlan {
     int mb;
-    int kts;
-    int splits;
+    int nsteps;  // steps of 4 k-slices per wave
+    int kw;      // k waves per workgroup
+    int splits;  // workgroups along k
 };
 
 int env_int(const char* name, int dflt) {
@@ -49,31 +50,43 @@ int env_int(const char* name, int dflt) {
     return atoi(v);
 }
 
-// gfx950 launch shape: every workgroup covers a 128-column block (one output
-// FWHT block) and `kts` k-slices.  The split count is the smallest that
-// still gives at least `target` workgroups (256 CUs, a few resident each),
-// so per-workgroup fixed costs (input rotation, reduction) stay small.
+// gfx950 launch shape.  Every workgroup covers one 128-column block (one
+// output FWHT block) with 4 column waves, times kw k-waves, each walking
+// `nsteps` steps of 4 k-slices.  Walk from the most work per wave to the least
+// and take the first shape that puts at least `target` waves on the device
+// (1024 SIMDs: ~3 waves each hide HBM and MFMA latency); this also keeps the
+// number of cross-workgroup k-splits (the costly reduction) minimal.
 GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
     GemvPlan pl;
     pl.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     const int kslices = k / 16;
-    const int max_kts = 4 * (K <= 4 ? 8 : 4);
-    const long long target = env_int("EXL3_GEMV_TARGET_WGS", 1024);
-    const int forced = env_int("EXL3_GEMV_KTS", 0);
+    const int max_steps = 16;
+    const long long target = env_int("EXL3_GEMV_TARGET_WAVES", 3072);
+    const int f_steps = env_int("EXL3_GEMV_NSTEPS", 0), f_kw = env_int("EXL3_GEMV_KW", 0);
     const long long cols = (long long)(n / 128) * experts;
-    int best = 8;
-    for (int kts = 8; kts <= max_kts && kts <= kslices; kts += 8) {
-        if (kslices % kts) continue;
-        if (gemv_smem_bytes(m, kts) > kMaxGemvSmem) continue;
-        if (forced > 0) {
-            if (kts == forced) best = kts;
-            continue;
+    GemvPlan best{pl.mb, 0, 0, 0};
+    long long best_waves = -1;
+    for (int kw = 2; kw >= 1; --kw) {
+        for (int ns = max_steps; ns >= 2; ns /= 2) {  // instantiated step counts: 16, 8, 4, 2
+            const int kts_wg = 4 * ns * kw;
+            if (kts_wg % 8 || kslices % kts_wg) continue;
+            if (gemv_smem_bytes(m, kts_wg, kw) > kMaxGemvSmem) continue;
+            if ((f_steps && ns != f_steps) || (f_kw && kw != f_kw)) continue;
+            const int S = kslices / kts_wg;
+            const long long waves = cols * S * 4 * kw;
+            if (waves >= target) {
+                if (best_waves < target || S < best.splits) {
+                    best = GemvPlan{pl.mb, ns, kw, S};
+                    best_waves = waves;
+                }
+            } else if (best_waves < target && waves > best_waves) {
+                best = GemvPlan{pl.mb, ns, kw, S};
+                best_waves = waves;
+            }
         }
-        if (cols * (kslices / kts) >= target || kts == 8) best = kts;
     }
-    pl.kts = best;
-    pl.splits = kslices / best;
-    return pl;
+    if (best.nsteps == 0) best = GemvPlan{pl.mb, 2, 1, kslices / 8};  // 128-row ranges always fit
+    return best;
 }
 
 size_t workspace_bytes_for(const GemvPlan& pl, int m, int n, int experts) {
@@ -97,7 +110,8 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
     const size_t need = workspace_bytes_for(pl, p.m, p.n, experts);
     EXL3_REQUIRE_CODE(need == 0 || (ws && ws_bytes >= need), EXL3_ERR_WORKSPACE,
                       "%s: workspace of %zu bytes needed, %zu given", fn, need, ws ? ws_bytes : (size_t)0);
-    p.kts = pl.kts;
+    p.nsteps = pl.nsteps;
+    p.kw = pl.kw;
     p.splits = pl.splits;
     if (need) {
         EXL3_REQUIRE_CODE((size_t)(p.n / 128) * experts <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
@@ -136,6 +150,21 @@ extern "C" size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int exper
     const int mc = m > kMaxGemvRows ? kMaxGemvRows : m;
     GemvPlan pl = plan_gemv(mc, k, n, K, experts);
     return workspace_bytes_for(pl, mc, n, experts);
+}
+
+extern "C" int exl3_gemv_plan(int m, int k, int n, int K, int experts, int* out) {
+    clear_error();
+    EXL3_REQUIRE(out, "exl3_gemv_plan: null pointer");
+    int rc = check_common("exl3_gemv_plan", m > kMaxGemvRows ? kMaxGemvRows : m, k, n, K, 1);
+    if (rc) return rc;
+    const int mc = m > kMaxGemvRows ? kMaxGemvRows : m;
+    GemvPlan pl = plan_gemv(mc, k, n, K, experts);
+    out[0] = pl.mb;
+    out[1] = pl.nsteps;
+    out[2] = pl.kw;
+    out[3] = pl.splits;
+    out[4] = (int)gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw);
+    return EXL3_OK;
 }
 
 extern "C" int exl3_gemv(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,

@@ -6,19 +6,20 @@
 // rotation, decode + product, k-split reduce, output rotation).
 //
 // Layout of the work:
-//   grid = (n/128 column blocks, S k-splits, E experts), 256 threads (4 waves).
-//   Wave w of a workgroup owns output columns [32w, 32w+32) of its block and
-//   walks the block's k-split 4 k-slices (one "step") at a time.  In a step,
-//   lane L = 16g + i decodes group q = i%8 of tile (kt0 + g, nt0 + i/8): 32
-//   values = MFMA B fragments for columns q and q+8, both k runs, giving four
-//   v_mfma_f32_16x16x32_f16 per 16-row block of x.  The MFMA's 32-deep k
-//   index (g, e) is the same permutation of tile rows for the A side (x',
-//   staged in LDS in that order) and the B side (the decode order), so the
-//   contraction is exact whatever order the tile stores k in.
-//   All weight loads of the wave are issued before the input-rotation prologue
-//   so HBM latency overlaps it.
-//   k-split partial sums go to the workspace; the last workgroup of a column
-//   block (atomic counter, self-resetting) sums them in split order
+//   grid = (n/128 column blocks, S k-splits, E experts); a workgroup has
+//   4*KW waves: wave w owns output columns [32(w%4), +32) of the block and the
+//   (w/4)-th of KW consecutive k ranges of the split.  Per step a wave covers
+//   4 k-slices x 2 column tiles: lane L = 16g + i decodes group q = i%8 of
+//   tile (kt + g, nt0 + i/8) -> 32 "pair-form" words (two fp16 numbers each,
+//   see exl3_decode.h) = 8 MFMA B fragments (2 columns x 4 quarters of k).
+//   The activation x' is staged in LDS in the matching A-fragment order with
+//   every value duplicated into both halves of a word, so each
+//   v_mfma_f32_16x16x32_f16 adds x'*(lo + hi) exactly in fp32.
+//   Activation loads are issued before the weight loads, and all weight loads
+//   of a wave are in flight while the input rotation runs.
+//   k ranges of the KW waves are summed through LDS; k-split partial sums go
+//   to the workspace through device-coherent stores; the last workgroup of a
+//   column block (atomic counter, self-resetting) sums them in split order
 //   (deterministic), applies the output FWHT and svh, and stores fp16.
 #pragma once
 
@@ -27,7 +28,8 @@
 
 namespace exl3 {
 
-constexpr int GV_THREADS = 256;
+constexpr int GV_MAX_THREADS = 512;  // 4 column waves x up to 2 k waves
+constexpr int GV_PRE = 8;            // rotation blocks per wave whose activations are preloaded
 
 struct GemvParams {
     const __half* x;
@@ -44,14 +46,24 @@ struct GemvParams {
     float* partials;  // [E][n/128][S][m][128]
     int* counters;    // [E][n/128]
     int m, k, n;
-    int kts;     // k-slices (16 rows each) per split, multiple of 8
-    int splits;  // S
+    int nsteps;  // steps (4 k-slices each) per wave
+    int kw;      // waves along k inside a workgroup (1 or 2)
+    int splits;  // S: workgroups along k
 };
 
-// Register budget for the weight words a wave keeps in flight.
+// Steps of weight words a wave keeps in flight (register budget: depth * K words).
 template <int K>
-__host__ __device__ constexpr int gv_max_steps() {
-    return K <= 4 ? 8 : 4;
+__host__ __device__ constexpr int gv_depth() {
+    return K <= 4 ? 4 : 2;
+}
+
+// fp16 pair from global memory (loaded as a 32-bit word).
+__device__ __forceinline__ __half2 ld_h2(const EXL3_GLOBAL __half* p) {
+    const uint32_t u = *reinterpret_cast<const EXL3_GLOBAL uint32_t*>(p);
+    return *reinterpret_cast<const __half2*>(&u);
+}
+__device__ __forceinline__ void st_h2(EXL3_GLOBAL __half* p, __half2 v) {
+    *reinterpret_cast<EXL3_GLOBAL uint32_t*>(p) = *reinterpret_cast<const uint32_t*>(&v);
 }
 
 __device__ __forceinline__ void fwht128_pair_f(float& a, float& b, int lane) {
@@ -82,27 +94,31 @@ __device__ __forceinline__ float coherent_load(const float* p) {
 // Wait until this wave's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Position (in halves) of x'[row][kk] (kk = k offset inside the split's range)
-// in the A-fragment order of the LDS staging buffer [kts][2][m][8].
-__device__ __forceinline__ int xs_index(int kk, int row, int m) {
-    const int ktl = kk >> 4, kw = kk & 15;
-    const int h = (kw >> 2) & 1, kp = kw - 4 * h;
+// Position (in halves) of the first copy of x'[row][kk] (kk = k offset inside
+// the workgroup's range) in the A-fragment staging buffer [m][kts][4][8]:
+// quarter Q / slot t of tile row kw = kk % 16 (kw = quarter_row(Q, t)).  Row
+// outermost, so a lane's fragments for successive steps and quarters sit at
+// compile-time offsets from one base address.
+__device__ __forceinline__ int xs_index(int kk, int row, int kts) {
+    const int ktl = kk >> 4, kwr = kk & 15;
+    const int h = (kwr >> 2) & 1, kp = kwr - 4 * h;
     const int e = (kp & 1) + 2 * ((kp >> 3) & 1) + 4 * ((kp >> 1) & 1);
-    return ((ktl * 2 + h) * m + row) * 8 + e;
+    const int Q = 2 * h + (e >> 2), t = e & 3;
+    return ((row * kts + ktl) * 4 + Q) * 8 + 2 * t;
 }
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 template <int K>
-__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
+__device__ __forceinline__ void load_words(const EXL3_GLOBAL uint32_t* p, uint32_t* w) {
     if constexpr (K == 4 || K == 8) {
 #pragma unroll
         for (int h = 0; h < K / 4; ++h) {
-            u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p) + h);
+            u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const EXL3_GLOBAL u32x4_t*>(p) + h);
             w[4 * h + 0] = v.x; w[4 * h + 1] = v.y; w[4 * h + 2] = v.z; w[4 * h + 3] = v.w;
         }
     } else if constexpr (K == 2) {
-        u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+        u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const EXL3_GLOBAL u32x2_t*>(p));
         w[0] = v.x; w[1] = v.y;
     } else {
 #pragma unroll
@@ -110,9 +126,9 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
     }
 }
 
-template <int K, int CB, int MB>
-__global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
-    constexpr int MS = gv_max_steps<K>();
+template <int K, int CB, int MB, int NS>
+__global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
+    constexpr int D = gv_depth<K>();
     extern __shared__ __align__(16) unsigned char gv_smem[];
 
     const int e = blockIdx.z, bx = blockIdx.x, sidx = blockIdx.y;
@@ -120,52 +136,90 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
     const __half* suh;
     const __half* svh;
     if (p.t_tab) {
-        const int id = p.ids[e];
-        trellis = reinterpret_cast<const uint32_t*>(p.t_tab[id]);
-        suh = reinterpret_cast<const __half*>(p.su_tab[id]);
-        svh = reinterpret_cast<const __half*>(p.sv_tab[id]);
+        const int id = gptr(p.ids)[e];
+        trellis = reinterpret_cast<const uint32_t*>(gptr(p.t_tab)[id]);
+        suh = reinterpret_cast<const __half*>(gptr(p.su_tab)[id]);
+        svh = reinterpret_cast<const __half*>(gptr(p.sv_tab)[id]);
     } else {
         trellis = p.trellis;
         suh = p.suh;
         svh = p.svh;
     }
-    const __half* x = p.x + (long long)e * p.x_stride_e;
-    const int m = p.m, k = p.k, n = p.n, kts = p.kts;
-    const int ntiles = n >> 4, nsteps = kts >> 2;
+    const EXL3_GLOBAL __half* x = gptr(p.x + (long long)e * p.x_stride_e);
+    const EXL3_GLOBAL __half* suhg = gptr(suh);
+    const int m = p.m, k = p.k, n = p.n, kw = p.kw;
+    constexpr int nsteps = NS;
+    const int nthreads = 256 * kw, nwaves = 4 * kw;
+    const int kts_wg = 4 * nsteps * kw;  // k-slices of this workgroup
+    const int ntiles = n >> 4;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int cw = wave & 3, kwi = wave >> 2;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
-    const int nt = bx * 8 + wave * 2 + (i >> 3);
-    const int kt0 = sidx * kts;
+    const int nt = bx * 8 + cw * 2 + (i >> 3);
+    const int kt_wg0 = sidx * kts_wg;
+    const int kt_w0 = kt_wg0 + kwi * 4 * nsteps;
 
-    // 1. issue every weight load of this wave
-    uint32_t w[MS][K];
-    {
-        const uint32_t* tb = trellis + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
-        const size_t step_stride = (size_t)4 * ntiles * (8 * K);
-#pragma unroll
-        for (int s = 0; s < MS; ++s)
-            if (s < nsteps) load_words<K>(tb + s * step_stride, w[s]);
-    }
-
-    // 2. input rotation of this split's k range into LDS (A-fragment order)
+    // LDS: x' in A order [m][kts_wg][4][8] halves, zero fragment, per-block
+    // sums of x' [m][kts_wg/8] (mul1 correction), partial tiles [kw][m][128]
+    const int nblk128 = kts_wg >> 3;
     _Float16* xs = reinterpret_cast<_Float16*>(gv_smem);
-    const int xs_halves = kts * 2 * m * 8;
-    float* ybuf = reinterpret_cast<float*>(gv_smem + ((xs_halves * 2 + 16 + 15) & ~15));
-    if (tid < 8) xs[xs_halves + tid] = (_Float16)0.0f;  // zero fragment for rows >= m
-    {
-        const int nblk = kts >> 3;  // 128-blocks in the split
-        for (int b = wave; b < m * nblk; b += GV_THREADS / 64) {
-            const int row = b / nblk, bb = b - row * nblk;
-            const int kk = bb * 128 + 2 * lane;
-            const int kg = kt0 * 16 + kk;
-            const __half2 xv = *reinterpret_cast<const __half2*>(x + (size_t)row * k + kg);
-            const __half2 sv = *reinterpret_cast<const __half2*>(suh + kg);
-            const __half2 pr = __hmul2(xv, sv);
-            float a = __low2float(pr), c = __high2float(pr);
-            fwht128_pair_f(a, c, lane);
-            xs[xs_index(kk, row, m)] = (_Float16)(a * kHadNorm);
-            xs[xs_index(kk + 1, row, m)] = (_Float16)(c * kHadNorm);
+    const int xs_halves = kts_wg * 4 * m * 8;
+    float* xsum = reinterpret_cast<float*>(gv_smem + (((size_t)xs_halves * 2 + 16 + 15) & ~(size_t)15));
+    float* ybuf = xsum + ((m * nblk128 + 3) & ~3);
+
+    // 1. activation loads of this wave's rotation blocks (up to GV_PRE of them),
+    //    then every weight load: the activations return first (in-order vmcnt)
+    const int nrot = m * nblk128;
+    __half2 xpre[GV_PRE], spre[GV_PRE];
+#pragma unroll
+    for (int j = 0; j < GV_PRE; ++j) {
+        const int b = wave + j * nwaves;
+        if (b < nrot) {
+            const int row = b / nblk128, bb = b - row * nblk128;
+            const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
+            xpre[j] = ld_h2(x + (size_t)row * k + kg);
+            spre[j] = ld_h2(suhg + kg);
         }
+    }
+    uint32_t w[D][K];
+    const EXL3_GLOBAL uint32_t* tb = gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + nt) * (8 * K) + K * q;
+    const size_t step_stride = (size_t)4 * ntiles * (8 * K);
+    // (loads are unconditional, clamped to the last step, so the number in
+    // flight is static and each use waits only for its own group)
+    constexpr int last = NS - 1;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < last ? d : last) * step_stride, w[d]);
+
+    // 2. input rotation of the workgroup's k range into LDS (A order, duplicated)
+    if (tid < 8) xs[xs_halves + tid] = (_Float16)0.0f;
+    auto rotate = [&](int b, __half2 xv, __half2 sv) {
+        const int row = b / nblk128, bb = b - row * nblk128;
+        const int kk = bb * 128 + 2 * lane;
+        const __half2 pr = __hmul2(xv, sv);
+        float a = __low2float(pr), c = __high2float(pr);
+        fwht128_pair_f(a, c, lane);
+        const _Float16 ha = (_Float16)(a * kHadNorm), hc = (_Float16)(c * kHadNorm);
+        const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
+        xs[ia] = ha;
+        xs[ia + 1] = ha;
+        xs[ic] = hc;
+        xs[ic + 1] = hc;
+        if constexpr (CB == 2) {
+            float t = (float)ha + (float)hc;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+            if (lane == 0) xsum[b] = t;
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < GV_PRE; ++j) {
+        const int b = wave + j * nwaves;
+        if (b < nrot) rotate(b, xpre[j], spre[j]);
+    }
+    for (int b = wave + GV_PRE * nwaves; b < nrot; b += nwaves) {
+        const int row = b / nblk128, bb = b - row * nblk128;
+        const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
+        rotate(b, ld_h2(x + (size_t)row * k + kg), ld_h2(suhg + kg));
     }
     __syncthreads();
 
@@ -176,39 +230,57 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
         acc[rb][0] = float4_t{0.f, 0.f, 0.f, 0.f};
         acc[rb][1] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
-    const int src_lane = (lane & ~7) | ((lane + 7) & 7);
-    int a_off[MB];
+    // lane holding the previous group of the same tile (q - 1 mod 8), as a
+    // ds_bpermute byte address
+    const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+    // A fragments: rows >= m read nothing and keep zeros
+    const _Float16* a_base[MB];
+    bool a_live[MB];
 #pragma unroll
     for (int rb = 0; rb < MB; ++rb) {
         const int row = rb * 16 + i;
-        a_off[rb] = row < m ? (g * 2 * m + row) * 8 : -1;
+        a_live[rb] = row < m;
+        a_base[rb] = xs + (size_t)((a_live[rb] ? row : 0) * kts_wg + kwi * 4 * nsteps + g) * 4 * 8;
     }
+    half8_t A[MB][4];
 #pragma unroll
-    for (int s = 0; s < MS; ++s) {
-        if (s < nsteps) {
-            uint32_t buf[K + 1];
-            buf[0] = __shfl(w[s][K - 1], src_lane);
+    for (int rb = 0; rb < MB; ++rb)
 #pragma unroll
-            for (int j = 0; j < K; ++j) buf[1 + j] = w[s][j];
-            uint32_t frag[2][2][4];
-            decode_group<K, CB, false>(buf, frag);
+        for (int Q = 0; Q < 4; ++Q) A[rb][Q] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    // software-pipelined stream, fully unrolled: each step decodes its words,
+    // then reuses their registers to request the words of step s + D, so D - 1
+    // groups stay in flight while it decodes
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+    for (int s = 0; s < NS; ++s) {
+        const int d = s % D;
+        uint32_t buf[K + 1];
 #pragma unroll
-                for (int rb = 0; rb < MB; ++rb) {
-                    const int off = a_off[rb] >= 0 ? a_off[rb] + (s * 4 * 2 * m + h * m) * 8 : xs_halves;
-                    const half8_t A = *reinterpret_cast<const half8_t*>(xs + off);
+        for (int j = 0; j < K; ++j) buf[1 + j] = w[d][j];
+        buf[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(prev_addr, (int)buf[K]);
+        uint32_t v[32];
+        decode_group_pairs<K, CB>(buf, v);
+        if (s + D < NS) load_words<K>(tb + (size_t)(s + D) * step_stride, w[d]);
 #pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const half8_t B = *reinterpret_cast<const half8_t*>(frag[c][h]);
-                        acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[rb][c], 0, 0, 0);
-                    }
+        for (int rb = 0; rb < MB; ++rb)
+            if (a_live[rb]) {
+#pragma unroll
+                for (int Q = 0; Q < 4; ++Q)
+                    A[rb][Q] = *reinterpret_cast<const half8_t*>(a_base[rb] + (s * 16 + Q) * 8);
+            }
+#pragma unroll
+        for (int Q = 0; Q < 4; ++Q) {
+#pragma unroll
+            for (int rb = 0; rb < MB; ++rb) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const half8_t B = *reinterpret_cast<const half8_t*>(&v[8 * Q + 4 * c]);
+                    acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb][Q], B, acc[rb][c], 0, 0, 0);
                 }
             }
         }
     }
 
-    // 4. per-block partial tile [m][128] into LDS
+    // 4. sum the KW k ranges through LDS: ybuf[kwi][m][128], then fold into ybuf[0]
 #pragma unroll
     for (int rb = 0; rb < MB; ++rb)
 #pragma unroll
@@ -216,9 +288,21 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = rb * 16 + 4 * g + r;
-                const int col = wave * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                if (row < m) ybuf[row * 128 + col] = acc[rb][c][r];
+                const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                if (row < m) ybuf[(kwi * m + row) * 128 + col] = acc[rb][c][r];
             }
+    __syncthreads();
+    for (int idx = tid; idx < m * 128; idx += nthreads) {
+        float v = ybuf[idx];
+        for (int j = 1; j < kw; ++j) v += ybuf[j * m * 128 + idx];
+        if constexpr (CB == 2) {
+            const int row = idx >> 7;
+            float sx = 0.f;
+            for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+            v = v * kMul1Kinv + kMul1Delta * sx;
+        }
+        ybuf[idx] = v;
+    }
     __syncthreads();
 
     // 5. k-split reduction (last workgroup of the column block finishes).
@@ -229,7 +313,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
     if (p.splits > 1) {
         const size_t cblk = (size_t)e * nblk_n + bx;
         float* part = p.partials + (cblk * p.splits + sidx) * (size_t)m * 128;
-        for (int idx = tid; idx < m * 128; idx += GV_THREADS) coherent_store(part + idx, ybuf[idx]);
+        for (int idx = tid; idx < m * 128; idx += nthreads) coherent_store(part + idx, ybuf[idx]);
         wait_stores();
         __syncthreads();
         __shared__ int is_last;
@@ -240,7 +324,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
         __syncthreads();
         if (!is_last) return;
         const float* base = p.partials + cblk * p.splits * (size_t)m * 128;
-        for (int idx = tid; idx < m * 128; idx += GV_THREADS) {
+        for (int idx = tid; idx < m * 128; idx += nthreads) {
             float sum = 0.f;
             for (int s2 = 0; s2 < p.splits; ++s2) sum += coherent_load(base + (size_t)s2 * m * 128 + idx);
             ybuf[idx] = sum;
@@ -250,38 +334,45 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_kernel(GemvParams p) {
     }
 
     // 6. output rotation, svh, fp16 store
-    __half* y = p.y + (long long)e * p.y_stride_e;
+    EXL3_GLOBAL __half* y = gptr(p.y + (long long)e * p.y_stride_e);
     const int c0 = bx * 128 + 2 * lane;
-    const __half2 svv = *reinterpret_cast<const __half2*>(svh + c0);
-    const float sv0 = __low2float(svv), sv1 = __high2float(svv);
-    for (int row = wave; row < m; row += GV_THREADS / 64) {
+    const __half2 svv = ld_h2(gptr(svh) + c0);
+    const float sva = __low2float(svv), svb = __high2float(svv);
+    for (int row = wave; row < m; row += nwaves) {
         float a = ybuf[row * 128 + 2 * lane], b = ybuf[row * 128 + 2 * lane + 1];
         fwht128_pair_f(a, b, lane);
-        const __half2 o = __floats2half2_rn(a * kHadNorm * sv0, b * kHadNorm * sv1);
-        *reinterpret_cast<__half2*>(y + (size_t)row * n + c0) = o;
+        const __half2 o = __floats2half2_rn(a * kHadNorm * sva, b * kHadNorm * svb);
+        st_h2(y + (size_t)row * n + c0, o);
     }
 }
 
-// Dynamic LDS bytes of gemv_kernel for (m, kts).
-inline size_t gemv_smem_bytes(int m, int kts) {
-    const size_t xs = ((size_t)kts * 2 * m * 8 * 2 + 16 + 15) & ~(size_t)15;
-    return xs + (size_t)m * 128 * 4;
+// Dynamic LDS bytes of gemv_kernel for (m, k-slices per workgroup, kw).
+inline size_t gemv_smem_bytes(int m, int kts_wg, int kw) {
+    const size_t xs = ((size_t)kts_wg * 4 * m * 8 * 2 + 16 + 15) & ~(size_t)15;
+    return xs + (size_t)((m * (kts_wg / 8) + 3) & ~3) * 4 + (size_t)kw * m * 128 * 4;
 }
 
 template <int K>
 int gemv_launch_k(int cb, int mb, const GemvParams& p, int experts, hipStream_t st) {
     dim3 grid(p.n / 128, p.splits, experts);
-    const size_t smem = gemv_smem_bytes(p.m, p.kts);
-#define EXL3_GV_CASE(CBV, MBV)                                                   \
-    if (cb == CBV && mb == MBV) {                                                \
-        gemv_kernel<K, CBV, MBV><<<grid, GV_THREADS, smem, st>>>(p);             \
-        return launch_status("exl3 gemv launch");                                \
+    const size_t smem = gemv_smem_bytes(p.m, 4 * p.nsteps * p.kw, p.kw);
+    const int threads = 256 * p.kw;
+#define EXL3_GV_NS(CBV, MBV, NSV)                                                                      \
+    if (cb == CBV && mb == MBV && p.nsteps == NSV) {                                                   \
+        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV>);                \
+        const int lrc = allow_dynamic_lds(fn, smem, "exl3 gemv");                                      \
+        if (lrc) return lrc;                                                                           \
+        gemv_kernel<K, CBV, MBV, NSV><<<grid, threads, smem, st>>>(p);                                 \
+        return launch_status("exl3 gemv launch");                                                      \
     }
+#define EXL3_GV_CASE(CBV, MBV) \
+    EXL3_GV_NS(CBV, MBV, 2) EXL3_GV_NS(CBV, MBV, 4) EXL3_GV_NS(CBV, MBV, 8) EXL3_GV_NS(CBV, MBV, 16)
     EXL3_GV_CASE(0, 1) EXL3_GV_CASE(0, 2) EXL3_GV_CASE(0, 4)
     EXL3_GV_CASE(1, 1) EXL3_GV_CASE(1, 2) EXL3_GV_CASE(1, 4)
     EXL3_GV_CASE(2, 1) EXL3_GV_CASE(2, 2) EXL3_GV_CASE(2, 4)
 #undef EXL3_GV_CASE
-    set_error("exl3 gemv: no kernel for codebook %d row blocks %d", cb, mb);
+#undef EXL3_GV_NS
+    set_error("exl3 gemv: no kernel for codebook %d row blocks %d steps %d", cb, mb, p.nsteps);
     return EXL3_ERR_UNSUPPORTED;
 }
 

@@ -35,6 +35,7 @@ SIGNATURES = {
     "exl3_decode_states": (_I, [_P, _I, _I, _I, _P, _P]),
     "exl3_decode_tiles": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
     "exl3_gemv_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
+    "exl3_gemv_plan": (_I, [_I, _I, _I, _I, _I, _P]),
     "exl3_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_p2b_gemv_batched": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
