@@ -24,7 +24,7 @@ ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
-    # packed-fp32 instructions stay off (see DESIGN: correctness hazard on these boxes)
+    # packed-fp32 instructions stay off (some packed forms have given silent wrong results on these boxes)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-Wno-pass-failed",
 ]

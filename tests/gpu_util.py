@@ -5,7 +5,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-# Tolerance bar of the matmul outputs (BASELINE north_star): max-abs-err <= 2e-2 * rms(ref)
+# Tolerance bar of the matmul outputs (north-star bar): max-abs-err <= 2e-2 * rms(ref)
 # and cosine >= 0.9999 against an fp32-accumulated reference on the same inputs.
 MAX_ABS_REL_RMS = 2e-2
 MIN_COSINE = 0.9999
@@ -15,7 +15,7 @@ CB_IDS = {"3inst": 0, "mcg": 1, "mul1": 2}
 
 def make_weight(k: int, n: int, K: int, seed: int):
     """Seeded EXL3 weight: uniform random int16 trellis (every 16-bit state reachable)
-    and +-1 fp16 sign vectors (SURVEY 8d recipe).  numpy arrays."""
+    and +-1 fp16 sign vectors.  numpy arrays."""
     rng = np.random.default_rng(seed)
     trellis = rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int64).astype(np.int16)
     suh = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)

@@ -1,9 +1,9 @@
 """GPU parity of exl3_gemv / exl3_gemm / p2b_gemv_batched against the CPU oracle.
 
-Bar (BASELINE north_star): max-abs-err <= 2e-2 * rms(ref) and cosine >= 0.9999
+Bar (north-star tolerance): max-abs-err <= 2e-2 * rms(ref) and cosine >= 0.9999
 against x @ dequant(W) accumulated in fp32 or better.  The dequantised W is the
 oracle's (bit-exact restatement of the reference host dequant); at the full
-BASELINE sizes the GPU dequant (pinned bit-exact in test_gpu_decode.py) stands in
+full sizes the GPU dequant (pinned bit-exact in test_gpu_decode.py) stands in
 for it, with a block spot-checked against the oracle.
 """
 
@@ -65,7 +65,7 @@ def _run_capi(xd, tr, su, sv, K, cb):
 
 @pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_gemv_baseline_config2_full_size(m):
-    """k=4096, n=14336, K=4, MCG, seeded random trellis, +-1 signs."""
+    """Headline config 2: k=4096, n=14336, K=4, MCG, seeded random trellis, +-1 signs."""
     print(f"case: gemv cfg2 full size m={m}", flush=True)
     k, n, K = 4096, 14336, 4
     trellis, suh, svh = make_weight(k, n, K, seed=2)

@@ -1,0 +1,228 @@
+"""Pins of the CPU oracle (oracle/exl3_oracle.c) — CPU only.
+
+Each oracle function is checked against something it does not restate:
+  * golden vectors written from the reference's own compiled decode header
+    (tests/golden/make_golden.py): codebook tables, windows, composed dequant;
+  * the reference header itself when oracle/_ref is built (exhaustive);
+  * closed forms: all-zero trellis, single-window tiles, Sylvester-matrix FWHT,
+    W = suh (.) svh (.) (H T H)/128 by numpy matrix products;
+  * brute force on tiny inputs (bit-serial window reader).
+"""
+
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _f16(bits):
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float64)
+
+
+# ------------------------------------------------------------------ codebooks
+
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_codebook_table_matches_reference_digest(cb):
+    g = np.load(os.path.join(GOLD, "codebooks.npz"))
+    table = oracle.codebook_table(cb, rtz=True)
+    assert hashlib.sha256(table.tobytes()).digest() == g[f"sha256_cb{cb}"].tobytes()
+    assert np.array_equal(table[g[f"states_cb{cb}"]], g[f"bits_cb{cb}"])
+
+
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_codebook_exhaustive_vs_reference_header(cb):
+    R = oracle.ref_lib()
+    if R is None:
+        pytest.skip("reference header not built here")
+    ref = np.array([R.ref_decode_codebook_bits(s, cb) for s in range(65536)], dtype=np.uint16)
+    assert np.array_equal(oracle.codebook_table(cb, rtz=True), ref)
+
+
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_rne_and_rtz_tables_bracket_the_exact_value(cb):
+    """Both tables round the same exact value: RTZ truncates toward 0,
+    RNE is the nearest fp16; they agree wherever the exact value is an fp16."""
+    exact = np.array([oracle.lib().orc_codebook_exact(s, cb) for s in range(0, 65536, 7)], dtype=np.float64)
+    rtz = _f16(oracle.codebook_table(cb, rtz=True)[::7])
+    rne = _f16(oracle.codebook_table(cb, rtz=False)[::7])
+    assert np.all(np.abs(rtz) <= np.abs(exact))
+    assert np.all(np.abs(rne - exact) <= np.abs(rtz - exact))
+    rep = exact.astype(np.float16).astype(np.float64) == exact
+    assert np.array_equal(rtz[rep], rne[rep])
+    ulp = np.spacing(np.abs(rtz).astype(np.float16)).astype(np.float64)  # upward from |rtz|
+    assert np.all(np.abs(rtz - exact) < ulp)
+
+
+def test_codebook_state_zero_closed_form():
+    """state 0: MCG -> 0x3b60 + 0x3b60 = 1.84375; mul1 -> 1024 * 0x1eee + 0xc931 = -3.453125."""
+    assert _f16(oracle.codebook_table(1, True)[0]) == 1.84375
+    assert _f16(oracle.codebook_table(2, True)[0]) == -3.453125
+
+
+def test_mul1_codebook_formula_by_integers():
+    """mul1 value = ((0x6400 + byte_sum(s*M)) as fp16) * 0x1eee + 0xc931, evaluated in exact
+    integer arithmetic: (1024 + S) * 1774 * 2^-18 - 2721792 * 2^-18."""
+    for s in range(0, 65536, 97):
+        x = (s * 0x83DCD12D) & 0xFFFFFFFF
+        S = sum((x >> (8 * i)) & 255 for i in range(4))
+        exact = ((1024 + S) * 1774 - 2721792) / 262144.0
+        assert oracle.lib().orc_codebook_exact(s, 2) == pytest.approx(exact, abs=0, rel=0)
+
+
+# -------------------------------------------------------------------- windows
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_read_window_matches_golden(K):
+    g = np.load(os.path.join(GOLD, "windows.npz"))
+    tile = g[f"tile_K{K}"]
+    got = np.array([oracle.read_window(tile, b) for b in range(256 * K)], dtype=np.uint16)
+    assert np.array_equal(got, g[f"win_K{K}"])
+
+
+@pytest.mark.parametrize("K", [1, 3, 4, 7])
+def test_read_window_brute_force_bitstream(K):
+    """16 bits starting at stream bit b of the cyclic MSB-first stream of LE uint32 words."""
+    rng = np.random.default_rng(K)
+    tile = rng.integers(0, 65536, size=16 * K, dtype=np.uint16)
+    words = tile.view(np.uint32)
+    bits = np.array([(int(w) >> (31 - i)) & 1 for w in words for i in range(32)], dtype=np.int64)
+    for b in range(0, 256 * K, 5):
+        want = 0
+        for i in range(16):
+            want = (want << 1) | int(bits[(b + i) % bits.size])
+        assert oracle.read_window(tile, b) == want
+
+
+# ----------------------------------------------------------------- tile layout
+
+@pytest.mark.parametrize("cb", [1, 2])
+def test_tile_layout_single_window(cb):
+    """A tile with exactly one value's window set to a distinct state: the decoded tile
+    differs from the all-zero tile at the one position the closed-form layout gives."""
+    K = 4
+    base = oracle.decode_tile(np.zeros(16 * K, dtype=np.uint16), K, cb, rtz=True)
+    for t in (0, 1, 7, 8, 37, 128, 200, 255):
+        # value t's window ends at bit (t+1)K: set the low bit of that window only
+        tile = np.zeros(16 * K, dtype=np.uint16)
+        bit = ((t + 1) * K - 1) % (256 * K)
+        word, off = divmod(bit, 32)
+        w = tile.view(np.uint32)
+        w[word] |= np.uint32(1 << (31 - off))
+        dec = oracle.decode_tile(tile, K, cb, rtz=True)
+        diff = np.argwhere(dec != base)
+        l, j = divmod(t, 8)
+        want_k = 2 * (l % 4) + (j & 1) + 8 * ((j >> 1) & 1)
+        want_n = l // 4 + 8 * (j >> 2)
+        # the window of value t contains that bit as its LSB; the next values' windows
+        # contain it too (shifted), so the changed set starts at t
+        assert [want_k, want_n] in diff.tolist()
+
+
+# --------------------------------------------------------------- hadamard
+
+def _sylvester(n):
+    H = np.array([[1.0]])
+    while H.shape[0] < n:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+def test_fwht_is_sylvester_product_and_involution():
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(128).astype(np.float32)
+    H = _sylvester(128)
+    assert np.allclose(oracle.fwht(v), H @ v.astype(np.float64), rtol=1e-5, atol=1e-4)
+    back = oracle.fwht(oracle.fwht(v)) / 128.0
+    assert np.allclose(back, v, atol=1e-5)
+
+
+def test_fwht_matches_reference_header_bitwise():
+    R = oracle.ref_lib()
+    if R is None:
+        pytest.skip("reference header not built here")
+    rng = np.random.default_rng(4)
+    for _ in range(20):
+        v = rng.standard_normal(128).astype(np.float32)
+        b = v.copy()
+        R.ref_hadamard(b.ctypes.data, 128)
+        assert np.array_equal(oracle.fwht(v).view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------------------- dequant
+
+@pytest.mark.parametrize("tag", ["K2_mcg", "K3_mul1", "K4_mcg", "K4_mul1", "K5_mcg", "K8_mul1"])
+def test_dequant_matches_golden_bits(tag):
+    g = np.load(os.path.join(GOLD, "dequant.npz"))
+    K = int(tag[1])
+    cb = 1 if tag.endswith("mcg") else 2
+    W = oracle.dequant(g[f"trellis_{tag}"], g[f"suh_{tag}"], g[f"svh_{tag}"], K, cb, rtz=True)
+    assert np.array_equal(W, g[f"W_{tag}"])
+
+
+def test_dequant_equals_matrix_form():
+    """W = suh (.) svh (.) (H T H) / 128 per 128-block, computed by dense matrix products
+    in float64 (a different algorithm); agreement within fp16 rounding."""
+    K, cb = 3, 1
+    rng = np.random.default_rng(9)
+    k, n = 256, 128
+    tr = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * K), dtype=np.uint16)
+    su = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+    sv = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+    T = np.zeros((k, n))
+    for kt in range(k // 16):
+        for nt in range(n // 16):
+            T[kt * 16:(kt + 1) * 16, nt * 16:(nt + 1) * 16] = _f16(oracle.decode_tile(tr[kt, nt], K, cb, rtz=True))
+    H = _sylvester(128)
+    Wm = np.zeros((k, n))
+    for r0 in range(0, k, 128):
+        for c0 in range(0, n, 128):
+            Wm[r0:r0 + 128, c0:c0 + 128] = H @ T[r0:r0 + 128, c0:c0 + 128] @ H / 128.0
+    Wm *= su.astype(np.float64)[:, None] * sv.astype(np.float64)[None, :]
+    W = _f16(oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    assert np.max(np.abs(W - Wm)) <= 2.0 ** -10 * np.max(np.abs(Wm)) + 1e-6
+
+
+def test_dequant_all_zero_trellis_closed_form():
+    """Reference fixture (tests/test_cuda_graph.py:76-78) at a dequant-valid size:
+    W = 128 c suh svh at each (128i, 128j) corner, 0 elsewhere."""
+    for cb, c in ((1, 1.84375), (2, -3.453125)):
+        k, n = 256, 384
+        rng = np.random.default_rng(2)
+        su = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+        sv = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+        W = _f16(oracle.dequant(np.zeros((k // 16, n // 16, 32), dtype=np.uint16), su, sv, 2, cb, rtz=True))
+        corner = W[::128, ::128]
+        want = 128.0 * c * np.outer(su[::128].astype(np.float64), sv[::128].astype(np.float64))
+        assert np.allclose(corner, want, rtol=1e-3)
+        mask = np.ones_like(W, dtype=bool)
+        mask[::128, ::128] = False
+        assert np.all(W[mask] == 0.0)
+
+
+def test_cpu_gemv_is_dequant_then_fp32_product():
+    rng = np.random.default_rng(1)
+    k, n, K = 256, 256, 4
+    tr = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * K), dtype=np.uint16)
+    su = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+    sv = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+    x = rng.standard_normal((2, k)).astype(np.float16)
+    y = oracle.cpu_gemv(x, tr, su, sv, K, 1)
+    W = _f16(oracle.dequant(tr, su, sv, K, 1, rtz=True))
+    assert np.allclose(y, x.astype(np.float64) @ W, rtol=1e-4, atol=1e-3)
+
+
+def test_swiglu_matches_formula():
+    g = np.array([-3.0, -0.5, 0.0, 0.7, 4.0], dtype=np.float32)
+    u = np.array([1.0, -2.0, 3.0, 0.5, -9.0], dtype=np.float32)
+    want = g / (1 + np.exp(-g)) * u
+    assert np.allclose(oracle.swiglu(g, u, float("inf")), want, rtol=1e-6)
+    L = 1.0
+    wl = np.minimum(g, L) / (1 + np.exp(-np.minimum(g, L))) * np.clip(u, -L, L)
+    assert np.allclose(oracle.swiglu(g, u, L), wl, rtol=1e-6)
+    for gi, ui in zip(g, u):
+        assert oracle.lib().orc_swiglu(float(gi), float(ui), 0.0) == pytest.approx(float(gi / (1 + np.exp(-gi)) * ui), rel=1e-6)
