@@ -83,6 +83,31 @@ def gemv_timing(torch, L, weights, m, steps, warmup):
     return e0.elapsed_time(e1) * 1e-3 / steps
 
 
+def profile_pass(torch, L, weights, steps):
+    """Eager (non-graph) launches for rocprofv3: `steps` m=1 GEMVs over the rotating
+    copies, then `steps` device copies of exactly one packed weight's bytes (the
+    calibration kernel whose FETCH_SIZE / WRITE_SIZE readings scale the counters)."""
+    k, n, K = K_DIM, N_DIM, BITS
+    x = torch.from_numpy(np.random.default_rng(101).standard_normal((1, k)).astype(np.float16)).cuda()
+    y = torch.empty((1, n), dtype=torch.float16, device="cuda")
+    ws = torch.zeros(max(int(L.exl3_gemv_workspace_size(1, k, n, K, 1)), 256), dtype=torch.uint8, device="cuda")
+    sp = int(torch.cuda.current_stream().cuda_stream)
+    for c in range(steps):
+        tr, su, sv = weights[c % NCOPY]
+        rc = L.exl3_gemv(x.data_ptr(), tr.data_ptr(), su.data_ptr(), sv.data_ptr(), y.data_ptr(), 1, k, n, K, 1,
+                         ws.data_ptr(), ws.numel(), sp)
+        if rc:
+            raise RuntimeError(L.exl3_last_error().decode())
+    torch.cuda.synchronize()
+    nbytes = k * n * K // 8
+    src = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(c) for c in range(NCOPY)]
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    for c in range(steps):
+        dst.copy_(src[c % NCOPY])
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_pass": True, "gemv_launches": steps, "copy_launches": steps, "copy_bytes": nbytes}))
+
+
 def cpu_baseline():
     """The reference's CPU exl3_gemv path (oracle restatement, one thread) on the full
     config-2 weight, m=1; median of 3 runs."""
@@ -113,6 +138,8 @@ def main():
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="eager m=1 launches plus a copy-kernel calibration, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
@@ -128,6 +155,10 @@ def main():
     for c in range(NCOPY):
         weights.append([torch.from_numpy(a).cuda() for a in make_weight(K_DIM, N_DIM, BITS, seed=c)])
     torch.cuda.synchronize()
+
+    if args.profile_pass:
+        profile_pass(torch, L, weights, args.steps)
+        return
 
     bytes_per_call = K_DIM * N_DIM * BITS // 8
     t1 = gemv_timing(torch, L, weights, 1, args.steps, args.warmup)
