@@ -83,6 +83,146 @@ def gemv_timing(torch, L, weights, m, steps, warmup):
     return e0.elapsed_time(e1) * 1e-3 / steps
 
 
+# ------------------------------------------------------------- MoE layer (config 4)
+
+MOE_E, MOE_TOPK, MOE_H, MOE_I, MOE_K = 128, 8, 2048, 768, 3
+MOE_LAYERS = 2  # 2 x 226 MB of expert weights > the 256 MB Infinity Cache
+
+
+def moe_routing(B, seed):
+    """Config-4 router: logits N(0,1) + log p_e, p_e ~ rank^-1.1 over a seeded
+    permutation of the experts; softmax, top-8, weights renormalised."""
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(MOE_E)
+    p = (np.arange(1, MOE_E + 1, dtype=np.float64) ** -1.1)[np.argsort(perm)]
+    p /= p.sum()
+    logits = rng.standard_normal((B, MOE_E)) + np.log(p)[None, :]
+    prob = np.exp(logits - logits.max(axis=1, keepdims=True))
+    prob /= prob.sum(axis=1, keepdims=True)
+    ids = np.argsort(-prob, axis=1)[:, :MOE_TOPK].astype(np.int32)
+    w = np.take_along_axis(prob, ids, axis=1)
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return ids, w
+
+
+class MoeWeights:
+    """One layer's experts in three stacked device tensors per projection
+    (trellis [E][k/16][n/16][16K], suh [E][k], svh [E][n]) plus the int64
+    pointer tables the kernels read."""
+
+    def __init__(self, torch, seed):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.t = {}
+        tabs = []
+        for proj, k, n in (("gate", MOE_H, MOE_I), ("up", MOE_H, MOE_I), ("down", MOE_I, MOE_H)):
+            tr = torch.randint(-32768, 32768, (MOE_E, k // 16, n // 16, 16 * MOE_K), dtype=torch.int16,
+                               device="cuda", generator=g)
+            su = (torch.randint(0, 2, (MOE_E, k), device="cuda", generator=g) * 2 - 1).half()
+            # output scale 4/sqrt(k) folded into svh (as checkpoints do) keeps activations O(1)
+            sv = ((torch.randint(0, 2, (MOE_E, n), device="cuda", generator=g) * 2 - 1) * (4.0 / k ** 0.5)).half()
+            self.t[proj] = (tr, su, sv)
+            for a in (tr, su, sv):
+                step = a[0].numel() * a.element_size()
+                tabs.append(torch.arange(MOE_E, dtype=torch.int64, device="cuda") * step + a.data_ptr())
+        self.tables = tabs
+
+
+def moe_loop(torch, x, ids_long, w, mw):
+    """Per-expert loop over the same GEMV kernels, shaped like the reference's
+    routed loop (src/sglang_exl3/exl3.py:520-576): unique experts on the host,
+    gather, gate/up/down linears, SwiGLU, weighted index_add."""
+    T = x.shape[0]
+    out = torch.zeros((T, MOE_H), dtype=torch.float32, device=x.device)
+    for e in torch.unique(ids_long).tolist():
+        tok, slot = (ids_long == e).nonzero(as_tuple=True)
+        h = x.index_select(0, tok)
+        gt, gs, gv = (a[e] for a in mw.t["gate"])
+        ut, us, uv = (a[e] for a in mw.t["up"])
+        dt, ds, dv = (a[e] for a in mw.t["down"])
+        gg = torch.ops.sglang_exl3.exl3_gemm(h, gt, gs, gv, MOE_K, True).float()
+        uu = torch.ops.sglang_exl3.exl3_gemm(h, ut, us, uv, MOE_K, True).float()
+        act = (torch.nn.functional.silu(gg) * uu).half()
+        d = torch.ops.sglang_exl3.exl3_gemm(act, dt, ds, dv, MOE_K, True).float()
+        out.index_add_(0, tok, d * w[tok, slot].unsqueeze(-1))
+    return out
+
+
+def moe_bench(torch, steps):
+    from sglang_exl3 import ops
+
+    ops.register_custom_ops()
+    layers = [MoeWeights(torch, 1000 + i) for i in range(MOE_LAYERS)]
+    torch.cuda.synchronize()
+    res = {}
+    for B in (1, 16, 64):
+        ids_np, w_np = moe_routing(B, seed=B)
+        U = len(np.unique(ids_np))
+        x = torch.from_numpy(np.random.default_rng(B + 5).standard_normal((B, MOE_H)).astype(np.float16)).cuda()
+        ids = torch.from_numpy(ids_np).cuda()
+        w = torch.from_numpy(w_np).cuda()
+
+        def layer(c):
+            return torch.ops.sglang_exl3.exl3_moe_layer(x, ids, w, *layers[c % MOE_LAYERS].tables, MOE_K, MOE_K,
+                                                        MOE_K, True, MOE_I, 0.0)
+
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for c in range(8):
+                layer(c)
+        torch.cuda.synchronize()
+        # eager: back-to-back calls, host launch cost included
+        n_eager = max(20, steps // 8)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for c in range(n_eager):
+                layer(c)
+            e1.record(stream)
+        e1.synchronize()
+        t_eager = e0.elapsed_time(e1) * 1e-3 / n_eager
+        # graph of `n` layer calls alternating the two layers
+        n = max(24, steps // 4)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for c in range(n):
+                    layer(c)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+        e1.synchronize()
+        t_graph = e0.elapsed_time(e1) * 1e-3 / n
+        # per-expert loop of the same kernels
+        ids_long = ids.long()
+        for c in range(2):
+            moe_loop(torch, x, ids_long, w, layers[c % MOE_LAYERS])
+        torch.cuda.synchronize()
+        n_loop = 6
+        t0 = time.perf_counter()
+        for c in range(n_loop):
+            moe_loop(torch, x, ids_long, w, layers[c % MOE_LAYERS])
+        torch.cuda.synchronize()
+        t_loop = (time.perf_counter() - t0) / n_loop
+        nbytes = U * (3 * MOE_H * MOE_I * MOE_K // 8)
+        res[f"B{B}"] = {
+            "unique_experts": U,
+            "us_per_layer_graph": round(t_graph * 1e6, 2),
+            "us_per_layer_eager": round(t_eager * 1e6, 2),
+            "tokens_per_s": round(B / t_graph, 1),
+            "GBps": round(nbytes / t_graph / 1e9, 1),
+            "pct_hbm_peak": round(100 * nbytes / t_graph / 1e9 / HBM_PEAK_GBS, 2),
+            "per_expert_loop_us": round(t_loop * 1e6, 1),
+            "speedup_vs_loop_eager": round(t_loop / t_eager, 2),
+        }
+    return res
+
+
 def profile_pass(torch, L, weights, steps):
     """Eager (non-graph) launches for rocprofv3: `steps` m=1 GEMVs over the rotating
     copies, then `steps` device copies of exactly one packed weight's bytes (the
@@ -138,6 +278,7 @@ def main():
     ap.add_argument("--steps", type=int, default=480)
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-moe", action="store_true", help="skip the batched-MoE layer leg")
     ap.add_argument("--profile-pass", action="store_true",
                     help="eager m=1 launches plus a copy-kernel calibration, for rocprofv3 counter runs")
     args = ap.parse_args()
@@ -201,6 +342,10 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "gemv_sweep": sweep,
     }
+    if not args.no_moe:
+        result["moe_layer"] = {"config": "config 4: E=128 top-8 hidden 2048 inter 768 K=3 MCG, "
+                                         f"{MOE_LAYERS} rotating layer copies",
+                               **moe_bench(torch, args.steps)}
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))

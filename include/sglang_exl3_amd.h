@@ -109,6 +109,50 @@ int exl3_p2b_gemv_batched(const uint16_t* x, int x_per_expert, const int64_t* tr
                           int num_active, uint16_t* out, int m, int k, int n, int K, int codebook,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scratch bytes exl3_moe_layer / exl3_p2b_fused_moe need for `tokens` tokens
+ * routed to `topk` of `num_experts` experts (hidden -> inter -> hidden).
+ * Zero-filled before first use; every call leaves its counters zero. */
+size_t exl3_moe_workspace_size(int tokens, int topk, int num_experts, int hidden, int inter);
+
+/* Launch shapes the planner picks for a MoE layer: out[0..3] = gate/up
+ * (row blocks, steps per wave, k waves, k-splits), out[4..7] = the same for
+ * down, out[8] = expert slots of the grid.  Replaces the occupancy-sized
+ * cooperative grid of csrc/p2b_moe.cu:364-378. */
+int exl3_moe_plan(int tokens, int topk, int num_experts, int hidden, int inter, int* out);
+
+/* Routed-expert MoE layer for a batch of tokens, one call, no host sync:
+ *   out[t] = sum_s w[t][s] * down_e( fp16( silu(min(g, L)) * clamp(u, -L, L) ) ),
+ *   e = topk_ids[t][s], g = fp16(gate_e(x[t])), u = fp16(up_e(x[t])),
+ * fp32 combine, fp16 out [tokens][hidden].  Ids outside [0, num_experts) are
+ * skipped (weight ignored), like map_topk_to_local's invalid slot.  The nine
+ * pointer tables are int64 device arrays of num_experts device addresses.
+ * swiglu_limit <= 0 or infinite: no clamp.  K per projection 1..8, one
+ * codebook; hidden, inter multiples of 128; tokens * topk <= 8192.
+ * Replaces the routed-expert paths of EXL3MoEMethod.apply
+ * (src/sglang_exl3/exl3.py:2253-2314 -> apply_exl3_experts :1347-1431 ->
+ * apply_exl3_python_loop :520-576 / apply_exl3_batched_moe_gemv :960-1110). */
+int exl3_moe_layer(const uint16_t* x, const int32_t* topk_ids, const float* topk_weights,
+                   const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                   const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                   const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                   int num_experts, uint16_t* out, int tokens, int topk, int hidden, int inter,
+                   int K_gate, int K_up, int K_down, int codebook, float swiglu_limit,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* One-token fused MoE: out[0] = fp16( sum_e rw[e] * down_{ids[e]}(...) ) as
+ * exl3_moe_layer with tokens = 1, topk = num_ids and fp16 routing weights;
+ * `out` [1][hidden] is overwritten.  Any hidden/inter multiple of 128 and any
+ * K per projection (the reference: hidden 4096, inter 1024/2048, equal K 2..4).
+ * Replaces p2b_fused_moe (csrc/bindings.cpp:158-167 -> csrc/p2b_moe.cu:417-468;
+ * torch op sglang_exl3::p2b_fused_moe, src/sglang_exl3/ops.py:121-184). */
+int exl3_p2b_fused_moe(const uint16_t* x, uint16_t* out, const int64_t* gate_trellis, const int64_t* gate_suh,
+                       const int64_t* gate_svh, const int64_t* up_trellis, const int64_t* up_suh,
+                       const int64_t* up_svh, const int64_t* down_trellis, const int64_t* down_suh,
+                       const int64_t* down_svh, int num_experts, const int32_t* expert_ids,
+                       const uint16_t* routing_weights, int num_ids, int hidden, int inter, int K_gate,
+                       int K_up, int K_down, int codebook, float swiglu_limit, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

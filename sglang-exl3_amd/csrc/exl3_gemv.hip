@@ -35,7 +35,7 @@ int gemv_launch(int K, int cb, int mb, const GemvParams& p, int experts, hipStre
 namespace {
 
 constexpr int kMaxGemvRows = 64;
-constexpr size_t kMaxGemvSmem = kMaxLds;
+constexpr size_t kMaxGemvSmem = kMaxLds - 1024;  // headroom for static LDS
 
 struct GemvPlan {
     int mb;

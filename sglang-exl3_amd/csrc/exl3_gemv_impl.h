@@ -126,6 +126,69 @@ __device__ __forceinline__ void load_words(const EXL3_GLOBAL uint32_t* p, uint32
     }
 }
 
+// Request the weight words of a wave's first D steps.  Loads are unconditional,
+// clamped to the last step, so the number in flight is static and each use
+// waits only for its own group.
+template <int K, int NS>
+__device__ __forceinline__ void prime_weights(uint32_t (&w)[gv_depth<K>()][K], const EXL3_GLOBAL uint32_t* tb,
+                                              size_t step_stride) {
+    constexpr int D = gv_depth<K>();
+    constexpr int last = NS - 1;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < last ? d : last) * step_stride, w[d]);
+}
+
+// The wave's NS steps: decode 4 k-slices x 2 column tiles per step into MFMA B
+// fragments and multiply with the staged activations.  Software-pipelined and
+// fully unrolled: each step decodes its words, then reuses their registers to
+// request the words of step s + D, so D - 1 groups stay in flight while it
+// decodes.  a_base[rb]: this lane's A fragments of row block rb in the LDS
+// staging buffer; rows with a_live false read nothing and multiply zeros.
+template <int K, int CB, int MB, int NS>
+__device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[gv_depth<K>()][K], const EXL3_GLOBAL uint32_t* tb,
+                                                  size_t step_stride, const _Float16* const (&a_base)[MB],
+                                                  const bool (&a_live)[MB], float4_t (&acc)[MB][2]) {
+    constexpr int D = gv_depth<K>();
+    const int lane = threadIdx.x & 63;
+    // lane holding the previous group of the same tile (q - 1 mod 8), as a
+    // ds_bpermute byte address
+    const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
+    half8_t A[MB][4];
+#pragma unroll
+    for (int rb = 0; rb < MB; ++rb)
+#pragma unroll
+        for (int Q = 0; Q < 4; ++Q) A[rb][Q] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int d = s % D;
+        uint32_t buf[K + 1];
+#pragma unroll
+        for (int j = 0; j < K; ++j) buf[1 + j] = w[d][j];
+        buf[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(prev_addr, (int)buf[K]);
+        uint32_t v[32];
+        decode_group_pairs<K, CB>(buf, v);
+        if (s + D < NS) load_words<K>(tb + (size_t)(s + D) * step_stride, w[d]);
+#pragma unroll
+        for (int rb = 0; rb < MB; ++rb)
+            if (a_live[rb]) {
+#pragma unroll
+                for (int Q = 0; Q < 4; ++Q)
+                    A[rb][Q] = *reinterpret_cast<const half8_t*>(a_base[rb] + (s * 16 + Q) * 8);
+            }
+#pragma unroll
+        for (int Q = 0; Q < 4; ++Q) {
+#pragma unroll
+            for (int rb = 0; rb < MB; ++rb) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const half8_t B = *reinterpret_cast<const half8_t*>(&v[8 * Q + 4 * c]);
+                    acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb][Q], B, acc[rb][c], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 template <int K, int CB, int MB, int NS>
 __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     constexpr int D = gv_depth<K>();
@@ -184,11 +247,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     uint32_t w[D][K];
     const EXL3_GLOBAL uint32_t* tb = gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + nt) * (8 * K) + K * q;
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
-    // (loads are unconditional, clamped to the last step, so the number in
-    // flight is static and each use waits only for its own group)
-    constexpr int last = NS - 1;
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < last ? d : last) * step_stride, w[d]);
+    prime_weights<K, NS>(w, tb, step_stride);
 
     // 2. input rotation of the workgroup's k range into LDS (A order, duplicated)
     if (tid < 8) xs[xs_halves + tid] = (_Float16)0.0f;
@@ -230,9 +289,6 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         acc[rb][0] = float4_t{0.f, 0.f, 0.f, 0.f};
         acc[rb][1] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
-    // lane holding the previous group of the same tile (q - 1 mod 8), as a
-    // ds_bpermute byte address
-    const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
     // A fragments: rows >= m read nothing and keep zeros
     const _Float16* a_base[MB];
     bool a_live[MB];
@@ -242,43 +298,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         a_live[rb] = row < m;
         a_base[rb] = xs + (size_t)((a_live[rb] ? row : 0) * kts_wg + kwi * 4 * nsteps + g) * 4 * 8;
     }
-    half8_t A[MB][4];
-#pragma unroll
-    for (int rb = 0; rb < MB; ++rb)
-#pragma unroll
-        for (int Q = 0; Q < 4; ++Q) A[rb][Q] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    // software-pipelined stream, fully unrolled: each step decodes its words,
-    // then reuses their registers to request the words of step s + D, so D - 1
-    // groups stay in flight while it decodes
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        const int d = s % D;
-        uint32_t buf[K + 1];
-#pragma unroll
-        for (int j = 0; j < K; ++j) buf[1 + j] = w[d][j];
-        buf[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(prev_addr, (int)buf[K]);
-        uint32_t v[32];
-        decode_group_pairs<K, CB>(buf, v);
-        if (s + D < NS) load_words<K>(tb + (size_t)(s + D) * step_stride, w[d]);
-#pragma unroll
-        for (int rb = 0; rb < MB; ++rb)
-            if (a_live[rb]) {
-#pragma unroll
-                for (int Q = 0; Q < 4; ++Q)
-                    A[rb][Q] = *reinterpret_cast<const half8_t*>(a_base[rb] + (s * 16 + Q) * 8);
-            }
-#pragma unroll
-        for (int Q = 0; Q < 4; ++Q) {
-#pragma unroll
-            for (int rb = 0; rb < MB; ++rb) {
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const half8_t B = *reinterpret_cast<const half8_t*>(&v[8 * Q + 4 * c]);
-                    acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb][Q], B, acc[rb][c], 0, 0, 0);
-                }
-            }
-        }
-    }
+    decode_mfma_steps<K, CB, MB, NS>(w, tb, step_stride, a_base, a_live, acc);
 
     // 4. sum the KW k ranges through LDS: ybuf[kwi][m][128], then fold into ybuf[0]
 #pragma unroll

@@ -26,6 +26,7 @@ CB_MUL1 = 2
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SZ = ctypes.c_size_t
+_F = ctypes.c_float
 
 # name -> (restype, argtypes); exactly the entry points include/sglang_exl3_amd.h declares
 SIGNATURES = {
@@ -39,6 +40,12 @@ SIGNATURES = {
     "exl3_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_p2b_gemv_batched": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "exl3_moe_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
+    "exl3_moe_plan": (_I, [_I, _I, _I, _I, _I, _P]),
+    "exl3_moe_layer": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I,
+                            _I, _I, _I, _I, _F, _P, _SZ, _P]),
+    "exl3_p2b_fused_moe": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I,
+                                _I, _I, _I, _I, _F, _P, _SZ, _P]),
 }
 
 _lib = None

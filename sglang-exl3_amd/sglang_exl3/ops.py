@@ -169,13 +169,107 @@ def p2b_gemv_batched_impl(x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices, K
     return out
 
 
+MOE_TABLE_NAMES = ("gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh",
+                   "down_trellis", "down_suh", "down_svh")
+
+
+def _moe_tables(name, tables):
+    if len(tables) != 9:
+        raise RuntimeError(f"sglang_exl3::{name}: nine pointer tables expected")
+    out = []
+    e = None
+    for t, what in zip(tables, MOE_TABLE_NAMES):
+        if t.dtype != torch.int64 or t.dim() != 1 or t.numel() == 0:
+            raise RuntimeError(f"sglang_exl3::{name}: {what} pointer table must be a nonempty 1-D int64 tensor")
+        if e is None:
+            e = t.numel()
+        elif t.numel() != e:
+            raise RuntimeError(f"sglang_exl3::{name}: pointer tables must be equally sized")
+        out.append(t.contiguous())
+    return out, int(e)
+
+
+def _limit_arg(swiglu_limit) -> float:
+    lim = float(swiglu_limit)
+    if lim != lim or lim < 0:
+        raise RuntimeError("sglang_exl3: SwiGLU limit must be nonnegative (0 or inf disables clipping)")
+    return lim
+
+
+def p2b_fused_moe_impl(x, out, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs,
+                       up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs, expert_indices,
+                       routing_weights, K_gate, K_up, K_down, mcg, intermediate_size=2048, swiglu_limit=0.0):
+    """One-token fused MoE (csrc/p2b_moe.cu:417-468 semantics; ABI-2 extras
+    intermediate_size / swiglu_limit as in csrc/bindings.cpp:192)."""
+    name = "p2b_fused_moe"
+    tables = (gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs,
+              down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs)
+    _require_device(name, x, out, expert_indices, routing_weights, *tables)
+    x = _f16(name, x, "x")
+    if out.dtype != torch.float16 or not out.is_contiguous() or tuple(out.shape) != tuple(x.shape):
+        raise RuntimeError(f"sglang_exl3::{name}: out must be a contiguous fp16 tensor shaped like x")
+    if x.dim() != 2 or int(x.shape[0]) != 1:
+        raise RuntimeError(f"sglang_exl3::{name}: one input row [1, hidden] expected")
+    ids = expert_indices.reshape(-1).to(torch.int32).contiguous()
+    rw = routing_weights.reshape(-1)
+    if rw.dtype != torch.float16 or rw.numel() != ids.numel() or ids.numel() == 0:
+        raise RuntimeError(f"sglang_exl3::{name}: one fp16 routing weight per (nonempty) expert index")
+    rw = rw.contiguous()
+    tabs, E = _moe_tables(name, tables)
+    hidden, inter = int(x.shape[1]), int(intermediate_size)
+    lib = _lib.lib()
+    with torch.cuda.device(x.device):
+        need = int(lib.exl3_moe_workspace_size(1, ids.numel(), E, hidden, inter))
+        ws = workspace(x.device, need)
+        rc = lib.exl3_p2b_fused_moe(
+            x.data_ptr(), out.data_ptr(), *[t.data_ptr() for t in tabs], E, ids.data_ptr(), rw.data_ptr(),
+            ids.numel(), hidden, inter, int(K_gate), int(K_up), int(K_down), _lib.codebook_from_mcg(bool(mcg)),
+            _limit_arg(swiglu_limit), ws.data_ptr(), ws.numel(), _stream_ptr(x))
+    _lib.check(rc, name)
+    return out
+
+
+def exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs,
+                        up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs,
+                        K_gate, K_up, K_down, mcg, intermediate_size, swiglu_limit=0.0):
+    """Routed-expert MoE layer for a token batch in one call (no host sync).
+    topk_ids: [T, topk] local expert ids (outside [0, E) = skipped);
+    topk_weights: [T, topk]; swiglu_limit 0 or inf = no clamp; returns fp16 [T, hidden]."""
+    name = "exl3_moe_layer"
+    tables = (gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs,
+              down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs)
+    _require_device(name, x, topk_ids, topk_weights, *tables)
+    if x.dim() != 2:
+        raise RuntimeError(f"sglang_exl3::{name}: x must be [tokens, hidden]")
+    T, hidden = int(x.shape[0]), int(x.shape[1])
+    ids = topk_ids.reshape(T, -1)
+    topk = int(ids.shape[1])
+    ids = ids.to(torch.int32).contiguous()
+    w = topk_weights.reshape(T, topk).to(torch.float32).contiguous()
+    xh = x.to(torch.float16).contiguous()
+    tabs, E = _moe_tables(name, tables)
+    out = torch.empty((T, hidden), dtype=torch.float16, device=x.device)
+    if T == 0 or topk == 0:
+        return out.zero_()
+    lim = _limit_arg(swiglu_limit)
+    lib = _lib.lib()
+    with torch.cuda.device(x.device):
+        need = int(lib.exl3_moe_workspace_size(T, topk, E, hidden, int(intermediate_size)))
+        ws = workspace(x.device, need)
+        rc = lib.exl3_moe_layer(
+            xh.data_ptr(), ids.data_ptr(), w.data_ptr(), *[t.data_ptr() for t in tabs], E, out.data_ptr(), T, topk,
+            hidden, int(intermediate_size), int(K_gate), int(K_up), int(K_down),
+            _lib.codebook_from_mcg(bool(mcg)), lim, ws.data_ptr(), ws.numel(), _stream_ptr(x))
+    _lib.check(rc, name)
+    return out
+
+
 def _not_built(name):
     def _fn(*args, **kwargs):
         raise RuntimeError(f"sglang_exl3::{name} is not implemented in this build")
     return _fn
 
 
-p2b_fused_moe_impl = _not_built("p2b_fused_moe")
 exl3_fat_gemm_impl = _not_built("exl3_fat_gemm")
 exl3_fat_gemm_scatter_impl = _not_built("exl3_fat_gemm_scatter")
 
@@ -248,6 +342,21 @@ def register_custom_ops() -> bool:
           down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs, expert_indices, routing_weights, K_gate, K_up,
           K_down, mcg):
         return None
+
+    @torch.library.custom_op("sglang_exl3::exl3_moe_layer", mutates_args=())
+    def exl3_moe_layer(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                       gate_trellis_ptrs: torch.Tensor, gate_suh_ptrs: torch.Tensor, gate_svh_ptrs: torch.Tensor,
+                       up_trellis_ptrs: torch.Tensor, up_suh_ptrs: torch.Tensor, up_svh_ptrs: torch.Tensor,
+                       down_trellis_ptrs: torch.Tensor, down_suh_ptrs: torch.Tensor, down_svh_ptrs: torch.Tensor,
+                       K_gate: int, K_up: int, K_down: int, mcg: bool, intermediate_size: int,
+                       swiglu_limit: float = 0.0) -> torch.Tensor:
+        return exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs,
+                                   up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs,
+                                   down_svh_ptrs, K_gate, K_up, K_down, mcg, intermediate_size, swiglu_limit)
+
+    @exl3_moe_layer.register_fake
+    def _(x, topk_ids, topk_weights, *rest):
+        return torch.empty((x.shape[0], x.shape[1]), dtype=torch.float16, device=x.device)
 
     @torch.library.custom_op("sglang_exl3::exl3_fat_gemm", mutates_args=("out",))
     def exl3_fat_gemm(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor, K: int,

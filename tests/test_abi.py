@@ -92,3 +92,32 @@ def test_codebook_flag_mapping_matches_reference():
     assert _lib.codebook_id(False, False) == 0 and _lib.codebook_id(False, True) == 2
     with pytest.raises(ValueError):
         _lib.codebook_id(True, True)
+
+
+def test_moe_plan_and_workspace_are_host_only():
+    L = _lib.lib()
+    out = (ctypes.c_int * 9)()
+    for T in (1, 16, 64):
+        assert L.exl3_moe_plan(T, 8, 128, 2048, 768, out) == 0
+        gu, dn, slots = list(out)[:4], list(out)[4:8], out[8]
+        assert slots == min(128, 8 * T)
+        for (mb, ns, kw, S), k in ((gu, 2048), (dn, 768)):
+            assert 16 * mb >= min(T, 64)
+            assert 4 * ns * kw * S == k // 16
+        assert L.exl3_moe_workspace_size(T, 8, 128, 2048, 768) > 256 * 1024
+    assert L.exl3_moe_workspace_size(0, 8, 128, 2048, 768) == 0
+
+
+def test_moe_rejects_bad_arguments_without_a_gpu():
+    L = _lib.lib()
+    nul = [None] * 9
+    rc = L.exl3_moe_layer(None, None, None, *nul, 128, None, 1, 8, 2048, 768, 3, 3, 3, 1, 0.0, None, 0, None)
+    assert rc == _lib.EXL3_ERR_ARG and b"null pointer" in L.exl3_last_error()
+    rc = L.exl3_moe_layer(1, 1, 1, *([1] * 9), 128, 1, 1, 8, 2000, 768, 3, 3, 3, 1, 0.0, None, 0, None)
+    assert rc == _lib.EXL3_ERR_ARG and b"multiples of 128" in L.exl3_last_error()
+    rc = L.exl3_moe_layer(1, 1, 1, *([1] * 9), 5000, 1, 1, 8, 2048, 768, 3, 3, 3, 1, 0.0, None, 0, None)
+    assert rc == _lib.EXL3_ERR_ARG and b"num_experts" in L.exl3_last_error()
+    rc = L.exl3_moe_layer(4, 4, 4, *([4] * 9), 128, 4, 1, 8, 2048, 768, 3, 3, 3, 1, 0.0, None, 0, None)
+    assert rc == _lib.EXL3_ERR_WORKSPACE
+    rc = L.exl3_p2b_fused_moe(1, 1, *([1] * 9), 8, 1, 1, 4, 2048, 768, 3, 3, 9, 1, 0.0, None, 0, None)
+    assert rc == _lib.EXL3_ERR_ARG and b"outside 1..8" in L.exl3_last_error()

@@ -1,0 +1,228 @@
+"""GPU parity of the batched MoE layer (exl3_moe_layer) and the one-token fused
+MoE (p2b_fused_moe) against the CPU oracle's routed loop.
+
+The oracle (oracle.moe_ref) follows src/sglang_exl3/exl3.py:520-576: per expert,
+gate/up linears of the fp16 tokens in fp32, silu(min(g, L)) * clamp(u, -L, L),
+the activation cast to fp16, the down linear, out[t] += w * down.  The GPU path
+rounds gate/up to fp16 as the batched reference path does (exl3.py:1018-1034);
+both sit inside the bar: max-abs-err <= 2e-2 * rms(ref), cosine >= 0.9999.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import check_close, make_weight, make_x
+from sglang_exl3 import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _registered():
+    ops.register_custom_ops()
+
+
+class Experts:
+    """E experts with seeded weights: numpy copies for the oracle, device tensors
+    kept alive behind int64 pointer tables (the layout of exl3.py:590-607)."""
+
+    def __init__(self, E, hidden, inter, Ks=(3, 3, 3), cb=1, seed=0):
+        self.E, self.hidden, self.inter, self.Ks, self.cb = E, hidden, inter, Ks, cb
+        self.np = []
+        self.dev = []
+        cols = {p: ([], [], []) for p in ("gate", "up", "down")}
+        for e in range(E):
+            spec = {}
+            for j, (proj, k, n) in enumerate((("gate", hidden, inter), ("up", hidden, inter), ("down", inter, hidden))):
+                K = Ks[j]
+                tr, su, sv = make_weight(k, n, K, seed=seed * 100003 + 3 * e + j)
+                # output scale folded into svh, as real checkpoints do, so that
+                # activations stay O(1) and fp16 never overflows: W ~ 4/sqrt(k)
+                sv = (sv.astype(np.float32) * (4.0 / np.sqrt(k))).astype(np.float16)
+                spec[proj] = (tr, su, sv, K, cb)
+                d = [torch.from_numpy(a).cuda() for a in (tr, su, sv)]
+                self.dev.append(d)
+                for c, t in zip(cols[proj], d):
+                    c.append(t.data_ptr())
+            self.np.append(spec)
+        self.tables = []
+        for proj in ("gate", "up", "down"):
+            for c in cols[proj]:
+                self.tables.append(torch.tensor(c, dtype=torch.int64, device="cuda"))
+
+    def layer(self, x, ids, w, limit=0.0):
+        KG, KU, KD = self.Ks
+        return torch.ops.sglang_exl3.exl3_moe_layer(x, ids, w, *self.tables, KG, KU, KD, self.cb == 1, self.inter,
+                                                    limit)
+
+    def ref(self, x_np, ids_np, w_np, limit=float("inf")):
+        return oracle.moe_ref(x_np, ids_np, w_np, self.np, limit)
+
+
+def _routing(T, topk, E, seed, invalid=0):
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(E, size=topk, replace=False) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, topk)).astype(np.float32) + 0.05
+    w /= w.sum(axis=1, keepdims=True)
+    for _ in range(invalid):
+        t, s = rng.integers(T), rng.integers(topk)
+        ids[t, s] = -1 if rng.random() < 0.5 else E + int(rng.integers(3))
+    return ids, w
+
+
+@pytest.mark.parametrize("T,topk,E,hidden,inter,Ks,cb", [
+    (1, 8, 16, 256, 256, (3, 3, 3), 1),
+    (1, 4, 8, 512, 384, (4, 4, 4), 2),
+    (4, 2, 8, 256, 256, (2, 2, 2), 1),
+    (7, 3, 6, 256, 128, (3, 4, 2), 1),      # per-projection K (gate != up -> two gate/up launches)
+    (16, 8, 32, 512, 256, (3, 3, 3), 1),
+    (33, 2, 4, 256, 256, (3, 3, 3), 2),     # 33 tokens over 4 experts: > 16 rows per expert
+    (80, 2, 2, 256, 128, (2, 2, 2), 1),     # > 64 rows per expert: several row passes
+    (5, 2, 4, 256, 256, (3, 3, 3), 0),      # 3INST codebook
+])
+def test_moe_layer_vs_oracle(T, topk, E, hidden, inter, Ks, cb):
+    print(f"case: moe T={T} topk={topk} E={E} h={hidden} i={inter} K={Ks} cb={cb}", flush=True)
+    ex = Experts(E, hidden, inter, Ks, cb, seed=T * 7 + E)
+    x = make_x(T, hidden, seed=T + 11)
+    ids, w = _routing(T, topk, E, seed=T * 3 + topk)
+    if cb == 0:
+        out = _layer_capi(ex, x, ids, w, cb=0)
+    else:
+        out = ex.layer(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    assert out.shape == (T, hidden) and out.dtype == torch.float16
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), f"moe T={T} E={E}")
+
+
+def _layer_capi(ex, x, ids, w, cb, limit=0.0):
+    T, hidden = x.shape
+    topk = ids.shape[1]
+    xd, idd, wd = (torch.from_numpy(a).cuda() for a in (x, ids, w))
+    out = torch.empty((T, hidden), dtype=torch.float16, device="cuda")
+    L = _lib.lib()
+    need = int(L.exl3_moe_workspace_size(T, topk, ex.E, hidden, ex.inter))
+    ws = ops.workspace(xd.device, need)
+    rc = L.exl3_moe_layer(xd.data_ptr(), idd.data_ptr(), wd.data_ptr(), *[t.data_ptr() for t in ex.tables], ex.E,
+                          out.data_ptr(), T, topk, hidden, ex.inter, *ex.Ks, cb, limit, ws.data_ptr(), ws.numel(),
+                          torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "exl3_moe_layer")
+    return out
+
+
+def test_moe_invalid_ids_are_skipped():
+    T, topk, E = 6, 4, 8
+    ex = Experts(E, 256, 256, (3, 3, 3), 1, seed=5)
+    x = make_x(T, 256, seed=3)
+    ids, w = _routing(T, topk, E, seed=9, invalid=5)
+    ids[2, :] = -1  # a token with no valid expert -> zero row
+    out = ex.layer(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda())
+    o = out.float().cpu().numpy()
+    assert np.all(o[2] == 0.0)
+    check_close(o, ex.ref(x, ids, w), "moe invalid ids")
+
+
+def test_moe_swiglu_limit():
+    """Gate values here have rms ~5, so L = 2 clamps many of them.  (A much
+    smaller L on much larger activations is ill-conditioned for any
+    implementation: there the reference's own RNE kernels and RTZ host dequant
+    differ by more than the bar, because the clamp turns fp16-level error of
+    large gate values into O(1) output error.)"""
+    T, topk, E = 3, 4, 8
+    ex = Experts(E, 256, 256, (4, 4, 4), 1, seed=6)
+    x = make_x(T, 256, seed=4)
+    ids, w = _routing(T, topk, E, seed=10)
+    lim = 2.0
+    out = ex.layer(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), lim)
+    o = out.float().cpu().numpy()
+    check_close(o, ex.ref(x, ids, w, lim), "moe limit")
+    unclamped = ex.ref(x, ids, w)
+    clamped = ex.ref(x, ids, w, lim)
+    rms = float(np.sqrt(np.mean(clamped ** 2)))
+    assert np.max(np.abs(unclamped - clamped)) > 0.1 * rms  # the clamp matters at this scale
+
+
+def test_moe_deterministic_and_graph_capturable():
+    T, topk, E = 16, 8, 32
+    ex = Experts(E, 512, 256, (3, 3, 3), 1, seed=8)
+    x = make_x(T, 512, seed=5)
+    ids, w = _routing(T, topk, E, seed=12)
+    xd, idd, wd = (torch.from_numpy(a).cuda() for a in (x, ids, w))
+    a = ex.layer(xd, idd, wd)
+    b = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    # capture into a HIP graph; replays interleaved with eager work must match
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ex.layer(xd, idd, wd)  # warm the per-stream workspace outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gout = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, a), f"graph replay {r} differs from eager"
+        ex.layer(xd, idd, wd)  # eager call on the default stream between replays
+        torch.cuda.synchronize()
+    # routing changes between replays are picked up (ids read on device)
+    ids2, w2 = _routing(T, topk, E, seed=13)
+    idd.copy_(torch.from_numpy(ids2))
+    wd.copy_(torch.from_numpy(w2))
+    g.replay()
+    torch.cuda.synchronize()
+    check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe graph new routing")
+
+
+def test_p2b_fused_moe_op():
+    """torch op with the reference schema: one token, fp16 routing weights, out overwritten."""
+    E, hidden, inter, topk = 12, 512, 256, 6
+    ex = Experts(E, hidden, inter, (2, 2, 2), 1, seed=21)
+    x = make_x(1, hidden, seed=8)
+    ids, w = _routing(1, topk, E, seed=14)
+    w16 = w.astype(np.float16)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.full_like(xd, 7.0)
+    ops.p2b_fused_moe_impl(xd, out, *ex.tables, torch.from_numpy(ids[0]).cuda(), torch.from_numpy(w16[0]).cuda(),
+                           2, 2, 2, True, intermediate_size=inter, swiglu_limit=0.0)
+    torch.cuda.synchronize()
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w16.astype(np.float32)), "p2b_fused_moe")
+    # through torch.ops with the reference's default intermediate size (2048)
+    ex2 = Experts(4, 256, 2048, (3, 3, 3), 1, seed=22)
+    x2 = make_x(1, 256, seed=9)
+    ids2, w2 = _routing(1, 2, 4, seed=15)
+    w2h = w2.astype(np.float16)
+    x2d = torch.from_numpy(x2).cuda()
+    out2 = torch.empty_like(x2d)
+    torch.ops.sglang_exl3.p2b_fused_moe(x2d, out2, *ex2.tables, torch.from_numpy(ids2[0]).cuda(),
+                                        torch.from_numpy(w2h[0]).cuda(), 3, 3, 3, True)
+    torch.cuda.synchronize()
+    check_close(out2.float().cpu().numpy(), ex2.ref(x2, ids2, w2h.astype(np.float32)), "p2b_fused_moe op")
+
+
+def test_moe_cfg4_batch16():
+    """Headline MoE shape (E=128, top-8, hidden 2048, inter 768, K=3, MCG) at B=16."""
+    T, topk, E = 16, 8, 128
+    ex = Experts(E, 2048, 768, (3, 3, 3), 1, seed=44)
+    x = make_x(T, 2048, seed=16)
+    ids, w = _routing(T, topk, E, seed=17)
+    out = ex.layer(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), "moe cfg4 B=16")
+
+
+def test_moe_rejects_bad_arguments():
+    ex = Experts(2, 256, 128, (2, 2, 2), 1, seed=1)
+    x = torch.zeros((1, 200), dtype=torch.float16, device="cuda")
+    ids = torch.zeros((1, 1), dtype=torch.int32, device="cuda")
+    w = torch.ones((1, 1), dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="multiples of 128"):
+        ex.layer(x, ids, w)
+    with pytest.raises(RuntimeError, match="K"):
+        torch.ops.sglang_exl3.exl3_moe_layer(torch.zeros((1, 256), dtype=torch.float16, device="cuda"), ids, w,
+                                             *ex.tables, 9, 2, 2, True, 128, 0.0)
