@@ -3,29 +3,31 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "exl3_moe_impl.h"
 
 namespace exl3 {
 
-int moe_launch_K1(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K2(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K3(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K4(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K5(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K6(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K7(int, int, int, const MoeParams&, dim3, hipStream_t);
-int moe_launch_K8(int, int, int, const MoeParams&, dim3, hipStream_t);
+int moe_launch_K1(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K2(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K3(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K4(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K5(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K6(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K7(int, int, const MoeParams&, hipStream_t);
+int moe_launch_K8(int, int, const MoeParams&, hipStream_t);
 
-int moe_launch(int K, int cb, int mb, int ns, const MoeParams& p, dim3 grid, hipStream_t st) {
+int moe_launch(int K, int cb, int ns, const MoeParams& p, hipStream_t st) {
     switch (K) {
-        case 1: return moe_launch_K1(cb, mb, ns, p, grid, st);
-        case 2: return moe_launch_K2(cb, mb, ns, p, grid, st);
-        case 3: return moe_launch_K3(cb, mb, ns, p, grid, st);
-        case 4: return moe_launch_K4(cb, mb, ns, p, grid, st);
-        case 5: return moe_launch_K5(cb, mb, ns, p, grid, st);
-        case 6: return moe_launch_K6(cb, mb, ns, p, grid, st);
-        case 7: return moe_launch_K7(cb, mb, ns, p, grid, st);
-        case 8: return moe_launch_K8(cb, mb, ns, p, grid, st);
+        case 1: return moe_launch_K1(cb, ns, p, st);
+        case 2: return moe_launch_K2(cb, ns, p, st);
+        case 3: return moe_launch_K3(cb, ns, p, st);
+        case 4: return moe_launch_K4(cb, ns, p, st);
+        case 5: return moe_launch_K5(cb, ns, p, st);
+        case 6: return moe_launch_K6(cb, ns, p, st);
+        case 7: return moe_launch_K7(cb, ns, p, st);
+        case 8: return moe_launch_K8(cb, ns, p, st);
     }
     set_error("exl3 moe: K=%d outside 1..8", K);
     return EXL3_ERR_UNSUPPORTED;
@@ -33,16 +35,22 @@ int moe_launch(int K, int cb, int mb, int ns, const MoeParams& p, dim3 grid, hip
 
 // ------------------------------------------------------------------ routing
 
-// Group the entries by expert.  Entries with ids outside [0, E) are dropped.
-// Row order inside an expert follows LDS atomics; each row's product is
-// independent of its position, so results do not depend on it.
+struct MoeTables {
+    const int64_t* t[9];  // gate trellis/suh/svh, up ..., down ...
+};
+
+// Group the entries by expert and cut each expert's rows into work units of
+// up to 16 rows, with the expert's nine weight addresses resolved.  Entries
+// with ids outside [0, E) are dropped.  Row order inside an expert follows
+// LDS atomics; each row's product is independent of its position, so results
+// do not depend on it.
 __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int32_t* ids, int entries, int E,
-                                                                     MoeRoute rt) {
+                                                                     MoeTables tabs, MoeRoute rt) {
     extern __shared__ __align__(16) int rt_smem[];
-    int* cnt = rt_smem;        // [E]
-    int* off = cnt + E;        // [E]
-    int* rank = off + E;       // [E]
-    int* pos = rank + E;       // [entries]
+    int* cnt = rt_smem;    // [E]
+    int* off = cnt + E;    // [E] first compact row
+    int* uoff = off + E;   // [E] first unit
+    int* pos = uoff + E;   // [entries]
     const int tid = threadIdx.x;
     for (int e = tid; e < E; e += MOE_ROUTE_THREADS) cnt[e] = 0;
     __syncthreads();
@@ -52,45 +60,61 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int3
         pos[i] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
     }
     __syncthreads();
-    // exclusive scans of counts and of "active" over the experts, one wave
+    // exclusive scans over the experts (rows, units, active), one wave
     if (tid < 64) {
         const int chunk = (E + 63) / 64;
         const int e0 = tid * chunk, e1 = min(E, e0 + chunk);
-        int sr = 0, sa = 0;
+        int sr = 0, su = 0, sa = 0;
         for (int e = e0; e < e1; ++e) {
-            sr += cnt[e];
-            sa += cnt[e] > 0;
+            const int c = cnt[e];
+            sr += c;
+            su += (c + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
+            sa += c > 0;
         }
-        int ir = sr, ia = sa;  // inclusive wave scan
+        int ir = sr, iu = su, ia = sa;  // inclusive wave scans
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
-            const int pr = __shfl_up(ir, d), pa = __shfl_up(ia, d);
+            const int pr = __shfl_up(ir, d), pu = __shfl_up(iu, d), pa = __shfl_up(ia, d);
             if (tid >= d) {
                 ir += pr;
+                iu += pu;
                 ia += pa;
             }
         }
-        int r = ir - sr, a = ia - sa;
+        int r = ir - sr, uu = iu - su;
         for (int e = e0; e < e1; ++e) {
             off[e] = r;
-            rank[e] = a;
+            uoff[e] = uu;
             r += cnt[e];
-            a += cnt[e] > 0;
+            uu += (cnt[e] + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
         }
-        if (tid == 63) gptr(rt.num_active)[0] = ia;
+        if (tid == 63) {
+            gptr(rt.counts)[0] = ia;
+            gptr(rt.counts)[1] = iu;
+        }
     }
     __syncthreads();
     for (int i = tid; i < entries; i += MOE_ROUTE_THREADS) {
-        const int p = pos[i];
-        if (p >= 0) gptr(rt.rows)[off[idg[i]] + p] = i;
+        const int ps = pos[i];
+        if (ps >= 0) gptr(rt.rows)[off[idg[i]] + ps] = i;
     }
     for (int e = tid; e < E; e += MOE_ROUTE_THREADS) {
         const int c = cnt[e];
-        if (c > 0) {
-            const int a = rank[e];
-            gptr(rt.act_expert)[a] = e;
-            gptr(rt.act_off)[a] = off[e];
-            gptr(rt.act_cnt)[a] = c;
+        if (c == 0) continue;
+        MoeUnit ud;
+        ud.e = e;
+        ud.pad = 0;
+        ud.pad2 = 0;
+#pragma unroll
+        for (int j = 0; j < 9; ++j) ud.ptr[j] = reinterpret_cast<const void*>(gptr(tabs.t[j])[e]);
+        const int nu = (c + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
+        for (int ch = 0; ch < nu; ++ch) {
+            ud.nrows = min(MOE_UNIT_ROWS, c - ch * MOE_UNIT_ROWS);
+            ud.crow0 = off[e] + ch * MOE_UNIT_ROWS;
+            const u32x4_t* src = reinterpret_cast<const u32x4_t*>(&ud);
+            EXL3_GLOBAL u32x4_t* dst = reinterpret_cast<EXL3_GLOBAL u32x4_t*>(gptr(rt.units) + uoff[e] + ch);
+#pragma unroll
+            for (int j = 0; j < (int)(sizeof(MoeUnit) / 16); ++j) dst[j] = src[j];
         }
     }
 }
@@ -120,13 +144,44 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const __half* y, const
     st_h2(gptr(out) + (size_t)t * hidden + c, __floats2half2_rn(a0, a1));
 }
 
+int moe_grid_size(const void* fn, int threads, size_t smem) {
+    struct Entry {
+        const void* fn;
+        int threads;
+        size_t smem;
+        int dev;
+        int grid;
+    };
+    static Entry cache[64];
+    static int ncache = 0;
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error("exl3 moe: hipGetDevice failed");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    for (int j = 0; j < ncache; ++j)
+        if (cache[j].fn == fn && cache[j].threads == threads && cache[j].smem == smem && cache[j].dev == dev)
+            return cache[j].grid;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        set_error("exl3 moe: occupancy query failed");
+        return -1;
+    }
+    const int grid = (per_cu < 1 ? 1 : per_cu) * (cus < 1 ? 1 : cus);
+    if (ncache < 64) cache[ncache++] = Entry{fn, threads, smem, dev, grid};
+    return grid;
+}
+
 namespace {
 
 constexpr int kMoeMaxExperts = 4096;
 constexpr int kMoeMaxEntries = 8192;
 
 struct MoePlan {
-    int mb, ns, kw, splits;
+    int ns, kw, splits;
 };
 
 int env_int(const char* name, int dflt) {
@@ -143,40 +198,45 @@ double expected_active(int tokens, int topk, int E) {
     return u < cap ? u : cap;
 }
 
-// Same rule as the dense GEMV planner: the most work per wave that still puts
-// `target` waves on the device, for the expected number of active experts.
-MoePlan plan_moe(int rows_cap, int k, int n, int nproj, double active) {
-    MoePlan pl{rows_cap <= 16 ? 1 : (rows_cap <= 32 ? 2 : 4), 0, 0, 0};
+// Launch shape of one expert projection pass.  Items = units x column blocks
+// x projections x k-splits; each item keeps 4 kw waves busy for ns steps.
+// From the most work per wave down, take the first shape with enough waves
+// for the device (`target`) whose split partials stay a small fraction of the
+// weight bytes; failing both, the best compromise.
+MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
     const int kslices = k / 16;
-    const long long target = env_int("EXL3_MOE_TARGET_WAVES", 3072);
+    const double target = env_int("EXL3_MOE_TARGET_WAVES", 3072);
+    const double max_traffic = env_int("EXL3_MOE_MAX_PARTIAL_PCT", 15) / 100.0;
     const int f_steps = env_int("EXL3_MOE_NSTEPS", 0), f_kw = env_int("EXL3_MOE_KW", 0);
-    const double cols = (double)(n / 128) * nproj * active;
-    MoePlan best = pl;
-    double best_waves = -1;
+    const double cols = (double)(n / 128) * nproj;
+    const double weight_bytes = units * cols * 128.0 * k * 4 / 8;  // nominal 4 bits
+    MoePlan best{0, 0, 0};
+    double best_score = -1;
     for (int kw = 2; kw >= 1; --kw) {
-        for (int ns = 8; ns >= 2; ns /= 2) {
+        for (int ns = 16; ns >= 2; ns /= 2) {
             const int kts_wg = 4 * ns * kw;
             if (kts_wg % 8 || kslices % kts_wg) continue;
-            if (moe_smem_bytes(pl.mb, kts_wg, kw) > kMaxLds - 1024) continue;  // headroom for static LDS
+            if (moe_smem_bytes(kts_wg, kw) > kMaxLds - 1024) continue;  // headroom for static LDS
             if ((f_steps && ns != f_steps) || (f_kw && kw != f_kw)) continue;
             const int S = kslices / kts_wg;
-            const double waves = cols * S * 4 * kw;
-            const bool better = waves >= target ? (best_waves < target || S < best.splits)
-                                                : (best_waves < target && waves > best_waves);
-            if (better) {
-                best = MoePlan{pl.mb, ns, kw, S};
-                best_waves = waves;
+            const double waves = units * cols * S * 4 * kw;
+            const double traffic = S > 1 ? 2.0 * entries * 512.0 * cols * S / weight_bytes : 0.0;
+            // 1 when both goals hold; otherwise the worse of the two ratios
+            const double score = fmin(1.0, fmin(waves / target, traffic > 0 ? max_traffic / traffic : 1.0));
+            if (score > best_score + 1e-9) {
+                best = MoePlan{ns, kw, S};
+                best_score = score;
             }
         }
     }
-    if (best.ns == 0) best = MoePlan{pl.mb, 2, 1, kslices / 8};
+    if (best.ns == 0) best = MoePlan{2, 1, kslices / 8};
     return best;
 }
 
 struct MoeLayout {
-    int slots, entries;
+    int entries, max_units;
     MoePlan gu, dn;
-    size_t route_off, h_off, y_off, part_off, total;
+    size_t route_off, units_off, rows_off, h_off, y_off, part_off, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -184,14 +244,20 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     MoeLayout L{};
     L.entries = tokens * topk;
-    L.slots = E < L.entries ? E : L.entries;
-    const int rows_cap = tokens < 64 ? tokens : 64;
+    const int slots = E < L.entries ? E : L.entries;
+    L.max_units = slots + (L.entries + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
     const double act = expected_active(tokens, topk, E);
-    L.gu = plan_moe(rows_cap, hidden, inter, 2, act);
-    L.dn = plan_moe(rows_cap, inter, hidden, 1, act);
+    const double per = act > 0 ? L.entries / act : 1.0;  // rows per active expert
+    const double units = act * ceil(per / MOE_UNIT_ROWS);
+    L.gu = plan_moe(units, L.entries, hidden, inter, 2);
+    L.dn = plan_moe(units, L.entries, inter, hidden, 1);
     size_t o = kWsCounterBytes;
     L.route_off = o;
-    o = align256(o + (size_t)(1 + 3 * L.slots + L.entries) * sizeof(int));
+    o = align256(o + 2 * sizeof(int));
+    L.units_off = o;
+    o = align256(o + (size_t)L.max_units * sizeof(MoeUnit));
+    L.rows_off = o;
+    o = align256(o + (size_t)L.entries * sizeof(int));
     L.h_off = o;
     o = align256(o + (size_t)L.entries * inter * 2);
     L.y_off = o;
@@ -203,10 +269,6 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     L.total = o;
     return L;
 }
-
-struct MoeTables {
-    const int64_t *gt, *gs, *gv, *ut, *us, *uv, *dt, *ds, *dv;
-};
 
 int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* weights, int weights_f16,
             const MoeTables& tb, int E, uint16_t* out, int tokens, int topk, int hidden, int inter, int KG,
@@ -220,25 +282,23 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     EXL3_REQUIRE(KG >= 1 && KG <= 8 && KU >= 1 && KU <= 8 && KD >= 1 && KD <= 8,
                  "%s: K (gate %d, up %d, down %d) outside 1..8", fn, KG, KU, KD);
     EXL3_REQUIRE(cb >= 0 && cb <= 2, "%s: codebook=%d outside 0..2", fn, cb);
-    EXL3_REQUIRE(x && ids && weights && out && tb.gt && tb.gs && tb.gv && tb.ut && tb.us && tb.uv && tb.dt &&
-                     tb.ds && tb.dv,
-                 "%s: null pointer", fn);
+    bool tabs_ok = true;
+    for (int j = 0; j < 9; ++j) tabs_ok = tabs_ok && tb.t[j];
+    EXL3_REQUIRE(x && ids && weights && out && tabs_ok, "%s: null pointer", fn);
     EXL3_REQUIRE(aligned(x, 4) && aligned(out, 4), "%s: misaligned x/out", fn);
     const MoeLayout L = moe_layout(tokens, topk, E, hidden, inter);
     EXL3_REQUIRE_CODE(ws && ws_bytes >= L.total, EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given",
                       fn, L.total, ws ? ws_bytes : (size_t)0);
     const int nblk_max = (hidden > inter ? hidden : inter) / 128;
-    EXL3_REQUIRE_CODE((size_t)L.slots * nblk_max <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
-                      "%s: %d slots x %d column blocks exceed the workspace counters", fn, L.slots, nblk_max);
+    EXL3_REQUIRE_CODE((size_t)L.max_units * nblk_max <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
+                      "%s: %d work units x %d column blocks exceed the workspace counters", fn, L.max_units,
+                      nblk_max);
 
     char* w8 = reinterpret_cast<char*>(ws);
     MoeRoute rt;
-    int* ri = reinterpret_cast<int*>(w8 + L.route_off);
-    rt.num_active = ri;
-    rt.act_expert = ri + 1;
-    rt.act_off = rt.act_expert + L.slots;
-    rt.act_cnt = rt.act_off + L.slots;
-    rt.rows = rt.act_cnt + L.slots;
+    rt.counts = reinterpret_cast<int*>(w8 + L.route_off);
+    rt.units = reinterpret_cast<MoeUnit*>(w8 + L.units_off);
+    rt.rows = reinterpret_cast<int*>(w8 + L.rows_off);
     __half* h = reinterpret_cast<__half*>(w8 + L.h_off);
     __half* yslots = reinterpret_cast<__half*>(w8 + L.y_off);
 
@@ -247,7 +307,7 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
         const size_t smem = moe_route_smem_bytes(E, L.entries);
         int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&moe_route_kernel), smem, "exl3 moe route");
         if (rc) return rc;
-        moe_route_kernel<<<1, MOE_ROUTE_THREADS, smem, st>>>(ids, L.entries, E, rt);
+        moe_route_kernel<<<1, MOE_ROUTE_THREADS, smem, st>>>(ids, L.entries, E, tb, rt);
         rc = launch_status("exl3 moe route launch");
         if (rc) return rc;
     }
@@ -264,13 +324,6 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     // 2. gate + up (+ SwiGLU + down input rotation)
     p.mode = MOE_GATE_UP;
     p.x = reinterpret_cast<const __half*>(x);
-    p.t_tab0 = tb.gt;
-    p.su_tab0 = tb.gs;
-    p.sv_tab0 = tb.gv;
-    p.t_tab1 = tb.ut;
-    p.su_tab1 = tb.us;
-    p.sv_tab1 = tb.uv;
-    p.dsu_tab = tb.ds;
     p.out = h;
     p.k = hidden;
     p.n = inter;
@@ -280,33 +333,31 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     int rc;
     if (KG == KU) {
         p.proj_base = 0;
-        rc = moe_launch(KG, cb, L.gu.mb, L.gu.ns, p, dim3(inter / 128, 2 * L.gu.splits, L.slots), st);
+        p.proj_launch = 2;
+        rc = moe_launch(KG, cb, L.gu.ns, p, st);
         if (rc) return rc;
     } else {
+        p.proj_launch = 1;
         p.proj_base = 0;
-        rc = moe_launch(KG, cb, L.gu.mb, L.gu.ns, p, dim3(inter / 128, L.gu.splits, L.slots), st);
+        rc = moe_launch(KG, cb, L.gu.ns, p, st);
         if (rc) return rc;
         p.proj_base = 1;
-        rc = moe_launch(KU, cb, L.gu.mb, L.gu.ns, p, dim3(inter / 128, L.gu.splits, L.slots), st);
+        rc = moe_launch(KU, cb, L.gu.ns, p, st);
         if (rc) return rc;
     }
 
     // 3. down
     p.mode = MOE_DOWN;
     p.x = h;
-    p.t_tab0 = tb.dt;
-    p.su_tab0 = tb.ds;
-    p.sv_tab0 = tb.dv;
-    p.t_tab1 = p.su_tab1 = p.sv_tab1 = nullptr;
-    p.dsu_tab = nullptr;
     p.out = yslots;
     p.k = inter;
     p.n = hidden;
     p.nproj = 1;
     p.proj_base = 0;
+    p.proj_launch = 1;
     p.splits = L.dn.splits;
     p.kw = L.dn.kw;
-    rc = moe_launch(KD, cb, L.dn.mb, L.dn.ns, p, dim3(hidden / 128, L.dn.splits, L.slots), st);
+    rc = moe_launch(KD, cb, L.dn.ns, p, st);
     if (rc) return rc;
 
     // 4. weighted combine
@@ -334,12 +385,12 @@ extern "C" int exl3_moe_plan(int tokens, int topk, int num_experts, int hidden, 
     const MoeLayout L = moe_layout(tokens, topk, num_experts, hidden, inter);
     const MoePlan* pls[2] = {&L.gu, &L.dn};
     for (int j = 0; j < 2; ++j) {
-        out[4 * j + 0] = pls[j]->mb;
+        out[4 * j + 0] = MOE_UNIT_ROWS;
         out[4 * j + 1] = pls[j]->ns;
         out[4 * j + 2] = pls[j]->kw;
         out[4 * j + 3] = pls[j]->splits;
     }
-    out[8] = L.slots;
+    out[8] = L.max_units;
     return EXL3_OK;
 }
 
@@ -351,7 +402,7 @@ extern "C" int exl3_moe_layer(const uint16_t* x, const int32_t* topk_ids, const 
                               int K_gate, int K_up, int K_down, int codebook, float swiglu_limit,
                               void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
-    MoeTables tb{gate_trellis, gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh};
+    MoeTables tb{{gate_trellis, gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh}};
     return run_moe("exl3_moe_layer", x, topk_ids, topk_weights, 0, tb, num_experts, out, tokens, topk, hidden,
                    inter, K_gate, K_up, K_down, codebook, swiglu_limit, workspace, workspace_bytes,
                    as_stream(stream));
@@ -365,7 +416,7 @@ extern "C" int exl3_p2b_fused_moe(const uint16_t* x, uint16_t* out, const int64_
                                   int hidden, int inter, int K_gate, int K_up, int K_down, int codebook,
                                   float swiglu_limit, void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
-    MoeTables tb{gate_trellis, gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh};
+    MoeTables tb{{gate_trellis, gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh}};
     return run_moe("exl3_p2b_fused_moe", x, expert_ids, routing_weights, 1, tb, num_experts, out, 1, num_ids,
                    hidden, inter, K_gate, K_up, K_down, codebook, swiglu_limit, workspace, workspace_bytes,
                    as_stream(stream));

@@ -10,7 +10,7 @@
 #define EXL3_CAT(a, b) EXL3_CAT2(a, b)
 
 namespace exl3 {
-int EXL3_CAT(moe_launch_K, EXL3_K)(int cb, int mb, int ns, const MoeParams& p, dim3 grid, hipStream_t st) {
-    return moe_launch_k<EXL3_K>(cb, mb, ns, p, grid, st);
+int EXL3_CAT(moe_launch_K, EXL3_K)(int cb, int ns, const MoeParams& p, hipStream_t st) {
+    return moe_launch_k<EXL3_K>(cb, ns, p, st);
 }
 }  // namespace exl3
