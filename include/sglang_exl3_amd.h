@@ -68,6 +68,16 @@ int exl3_decode_states(const uint16_t* states, int count, int codebook, int roun
 int exl3_decode_tiles(const int16_t* trellis, uint16_t* W, int k, int n, int K, int codebook,
                       int round_toward_zero, void* stream);
 
+/* Row-wise 128-point Hadamard transform, fp32 inside, fp16 in and out:
+ *   y[r][128c + j] = fp16( (H (x[r][128c..128c+127] (.) pre[128c..]))[j] * scale * post[128c + j] )
+ * with H the unnormalised Sylvester matrix (scale = 1/sqrt(128) normalises);
+ * pre / post may be NULL (no scaling).  x, y: f16 [rows][cols], cols a
+ * multiple of 128; y may alias x.  Replaces exllamav3's had_r_128 as called by
+ * src/sglang_exl3/exl3.py:1184-1228 and the matmul of transform_hadamard_fast
+ * (src/sglang_exl3/hadamard_cache.py:89-120). */
+int exl3_hadamard_rows(const uint16_t* x, uint16_t* y, const uint16_t* pre, const uint16_t* post, float scale,
+                       int rows, int cols, void* stream);
+
 /* Scratch bytes exl3_gemv / exl3_gemm / exl3_p2b_gemv_batched need for a
  * problem of `experts` independent GEMVs of [m,k]x[k,n].  The workspace must
  * be zero-filled before its first use; every call leaves it zero-filled again

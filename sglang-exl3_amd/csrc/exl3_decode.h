@@ -43,6 +43,78 @@ __device__ __forceinline__ EXL3_GLOBAL T* gptr(T* p) {
     return (EXL3_GLOBAL T*)p;
 }
 
+// ------------------------------------------------------- cross-lane moves
+
+// Value of v held by lane (lane ^ J) of the wave, J in {1, 2, 4, 8, 16, 32},
+// with DPP moves and the gfx950 permlane swaps: plain VALU, no LDS round trip
+// (the generic shuffle lowers to ds_bpermute).
+template <int J>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int iv = __float_as_int(v);
+    int r;
+    if constexpr (J == 1) {
+        r = __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (J == 2) {
+        r = __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (J == 4) {
+        const int t = __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false);  // row_half_mirror: lane ^ 7
+        r = __builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false);              // quad_perm [3,2,1,0]: ^ 3
+    } else if constexpr (J == 8) {
+        r = __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (J == 16) {
+        // rows 2r / 2r+1 exchanged: the first result holds the even row in
+        // both, the second the odd row in both
+        const auto sw = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+        r = (threadIdx.x & 16) ? (int)sw[0] : (int)sw[1];
+    } else {
+        static_assert(J == 32, "lane_xor: J must be a power of two below 64");
+        const auto sw = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        r = (threadIdx.x & 32) ? (int)sw[0] : (int)sw[1];
+    }
+    return __int_as_float(r);
+}
+
+template <int J>
+__device__ __forceinline__ void fwht_stage(float& a, float& b, int lane) {
+    const float pa = lane_xor<J>(a), pb = lane_xor<J>(b);
+    if (lane & J) {
+        a = pa - a;
+        b = pb - b;
+    } else {
+        a = a + pa;
+        b = b + pb;
+    }
+}
+
+// Unnormalised 128-point Walsh-Hadamard transform of one wave's 128 values,
+// value 2*lane in a and 2*lane+1 in b.  Radix-2 stages of stride 1, 2, ..., 64
+// in that order, each (x[i] + x[i+h], x[i] - x[i+h]): the same float
+// operations in the same order as the reference's hadamard
+// (csrc/exl3_dequant.cuh:137-148), so results are bit-identical.
+__device__ __forceinline__ void fwht128_pair_f(float& a, float& b, int lane) {
+    const float s = a + b, d = a - b;
+    a = s;
+    b = d;
+    fwht_stage<1>(a, b, lane);
+    fwht_stage<2>(a, b, lane);
+    fwht_stage<4>(a, b, lane);
+    fwht_stage<8>(a, b, lane);
+    fwht_stage<16>(a, b, lane);
+    fwht_stage<32>(a, b, lane);
+}
+
+// Sum of v over the 64 lanes of the wave (every lane gets the same total,
+// accumulated in a fixed order).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += lane_xor<32>(v);
+    v += lane_xor<16>(v);
+    v += lane_xor<8>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<1>(v);
+    return v;
+}
+
 // k offsets (inside a 16-row tile) of the 8 values one run gives one column,
 // in decode order; the second run adds 4.
 __host__ __device__ constexpr int kofs(int e) {

@@ -14,24 +14,6 @@ namespace {
 constexpr int DQ_THREADS = 256;
 constexpr int DQ_PITCH = 129;  // fp32 row pitch of the LDS block (bank spread)
 
-// In-register FWHT of one 128-vector held as (a, b) = elements (2l, 2l+1) of
-// lane l; stage order and operand order equal the scalar reference loop.
-__device__ __forceinline__ void fwht128_pair(float& a, float& b, int lane) {
-    float s = a + b, d = a - b;
-    a = s;
-    b = d;
-#pragma unroll
-    for (int j = 1; j < 64; j <<= 1) {
-        float pa = __shfl_xor(a, j), pb = __shfl_xor(b, j);
-        if (lane & j) {
-            a = pa - a;
-            b = pb - b;
-        } else {
-            a = a + pa;
-            b = b + pb;
-        }
-    }
-}
 
 template <int K, int CB>
 __global__ __launch_bounds__(DQ_THREADS) void dequant_kernel(const uint32_t* __restrict__ trellis,
@@ -75,7 +57,7 @@ __global__ __launch_bounds__(DQ_THREADS) void dequant_kernel(const uint32_t* __r
     // 2. row pass
     for (int r = wave; r < 128; r += DQ_THREADS / 64) {
         float a = M[r * DQ_PITCH + 2 * lane], b = M[r * DQ_PITCH + 2 * lane + 1];
-        fwht128_pair(a, b, lane);
+        fwht128_pair_f(a, b, lane);
         M[r * DQ_PITCH + 2 * lane] = a * kHadNorm;
         M[r * DQ_PITCH + 2 * lane + 1] = b * kHadNorm;
     }
@@ -87,7 +69,7 @@ __global__ __launch_bounds__(DQ_THREADS) void dequant_kernel(const uint32_t* __r
     const float su1 = __half2float(suh[r0 + 2 * lane + 1]);
     for (int c = wave; c < 128; c += DQ_THREADS / 64) {
         float a = M[(2 * lane) * DQ_PITCH + c], b = M[(2 * lane + 1) * DQ_PITCH + c];
-        fwht128_pair(a, b, lane);
+        fwht128_pair_f(a, b, lane);
         const float sv = __half2float(svh[c0 + c]);
         float va = a * kHadNorm;
         va = va * su0;

@@ -51,10 +51,12 @@ struct GemvParams {
     int splits;  // S: workgroups along k
 };
 
-// Steps of weight words a wave keeps in flight (register budget: depth * K words).
+// Steps of weight words a wave keeps in flight.  Measured on MI355X (config 2,
+// m=1): depth 2 is as fast as 4, 6 or 8 at every launch shape and the fastest
+// at the planner's shape; the fewer registers keep occupancy up.
 template <int K>
 __host__ __device__ constexpr int gv_depth() {
-    return K <= 4 ? 4 : 2;
+    return 2;
 }
 
 // fp16 pair from global memory (loaded as a 32-bit word).
@@ -64,23 +66,6 @@ __device__ __forceinline__ __half2 ld_h2(const EXL3_GLOBAL __half* p) {
 }
 __device__ __forceinline__ void st_h2(EXL3_GLOBAL __half* p, __half2 v) {
     *reinterpret_cast<EXL3_GLOBAL uint32_t*>(p) = *reinterpret_cast<const uint32_t*>(&v);
-}
-
-__device__ __forceinline__ void fwht128_pair_f(float& a, float& b, int lane) {
-    float s = a + b, d = a - b;
-    a = s;
-    b = d;
-#pragma unroll
-    for (int j = 1; j < 64; j <<= 1) {
-        float pa = __shfl_xor(a, j), pb = __shfl_xor(b, j);
-        if (lane & j) {
-            a = pa - a;
-            b = pb - b;
-        } else {
-            a = a + pa;
-            b = b + pb;
-        }
-    }
 }
 
 // Device-coherent (sc1) store/load: visible to every workgroup of the device
@@ -244,6 +229,9 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
             spre[j] = ld_h2(suhg + kg);
         }
     }
+    // output scale of this lane's two columns, requested now: the epilogue
+    // then needs no extra round trip
+    const __half2 svv = ld_h2(gptr(svh) + bx * 128 + 2 * lane);
     uint32_t w[D][K];
     const EXL3_GLOBAL uint32_t* tb = gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + nt) * (8 * K) + K * q;
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
@@ -264,9 +252,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         xs[ic] = hc;
         xs[ic + 1] = hc;
         if constexpr (CB == 2) {
-            float t = (float)ha + (float)hc;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+            const float t = wave_sum((float)ha + (float)hc);
             if (lane == 0) xsum[b] = t;
         }
     };
@@ -356,7 +342,6 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     // 6. output rotation, svh, fp16 store
     EXL3_GLOBAL __half* y = gptr(p.y + (long long)e * p.y_stride_e);
     const int c0 = bx * 128 + 2 * lane;
-    const __half2 svv = ld_h2(gptr(svh) + c0);
     const float sva = __low2float(svv), svb = __high2float(svv);
     for (int row = wave; row < m; row += nwaves) {
         float a = ybuf[row * 128 + 2 * lane], b = ybuf[row * 128 + 2 * lane + 1];

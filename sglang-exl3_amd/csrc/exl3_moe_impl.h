@@ -196,9 +196,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
             xs[ic] = hc;
             xs[ic + 1] = hc;
             if constexpr (CB == 2) {
-                float t = (float)ha + (float)hc;
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+                const float t = wave_sum((float)ha + (float)hc);
                 if (lane == 0) xsum[b] = t;
             }
         };
