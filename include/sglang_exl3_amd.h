@@ -125,8 +125,8 @@ int exl3_p2b_gemv_batched(const uint16_t* x, int x_per_expert, const int64_t* tr
 size_t exl3_moe_workspace_size(int tokens, int topk, int num_experts, int hidden, int inter);
 
 /* Launch shapes the planner picks for a MoE layer: out[0..3] = gate/up
- * (row blocks, steps per wave, k waves, k-splits), out[4..7] = the same for
- * down, out[8] = expert slots of the grid.  Replaces the occupancy-sized
+ * (column blocks per work item, steps per wave, k waves, k-splits),
+ * out[4..7] = the same for down, out[8] = bound on 16-row work units.  Replaces the occupancy-sized
  * cooperative grid of csrc/p2b_moe.cu:364-378. */
 int exl3_moe_plan(int tokens, int topk, int num_experts, int hidden, int inter, int* out);
 

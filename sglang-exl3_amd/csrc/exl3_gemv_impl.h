@@ -76,6 +76,31 @@ __device__ __forceinline__ void coherent_store(float* p, float v) {
 __device__ __forceinline__ float coherent_load(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Two adjacent floats through one device-coherent 8-byte load.
+__device__ __forceinline__ float2 coherent_load2(const float* p) {
+    const unsigned long long u = __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float*>(p)),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
+
+constexpr int GV_MAX_SPLITS = 16;  // k-splits a reduction reads in one round trip
+
+// sum_{s < S} p[s * stride] in split order.  The S device-coherent loads are
+// all issued before the first add, so the reduction costs one memory round
+// trip instead of S (S <= GV_MAX_SPLITS; larger S continues in groups).
+__device__ __forceinline__ float sum_splits(const float* p, size_t stride, int S) {
+    float sum = 0.f;
+    for (int s0 = 0; s0 < S; s0 += GV_MAX_SPLITS) {
+        float v[GV_MAX_SPLITS];
+#pragma unroll
+        for (int j = 0; j < GV_MAX_SPLITS; ++j) v[j] = (s0 + j < S) ? coherent_load(p + (size_t)(s0 + j) * stride) : 0.f;
+#pragma unroll
+        for (int j = 0; j < GV_MAX_SPLITS; ++j)
+            if (s0 + j < S) sum += v[j];
+    }
+    return sum;
+}
+
 // Wait until this wave's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -330,11 +355,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         __syncthreads();
         if (!is_last) return;
         const float* base = p.partials + cblk * p.splits * (size_t)m * 128;
-        for (int idx = tid; idx < m * 128; idx += nthreads) {
-            float sum = 0.f;
-            for (int s2 = 0; s2 < p.splits; ++s2) sum += coherent_load(base + (size_t)s2 * m * 128 + idx);
-            ybuf[idx] = sum;
-        }
+        for (int idx = tid; idx < m * 128; idx += nthreads) ybuf[idx] = sum_splits(base + idx, (size_t)m * 128, p.splits);
         if (tid == 0) __hip_atomic_store(p.counters + cblk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
     }

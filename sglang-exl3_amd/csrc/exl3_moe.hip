@@ -144,13 +144,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const __half* y, const
     st_h2(gptr(out) + (size_t)t * hidden + c, __floats2half2_rn(a0, a1));
 }
 
+static int env_int_once(const char* name) {
+    const char* v = getenv(name);
+    return (v && *v) ? atoi(v) : 0;
+}
+
 int moe_grid_size(const void* fn, int threads, size_t smem) {
     struct Entry {
         const void* fn;
         int threads;
         size_t smem;
         int dev;
-        int grid;
+        int per_cu, cus;
     };
     static Entry cache[64];
     static int ncache = 0;
@@ -160,19 +165,40 @@ int moe_grid_size(const void* fn, int threads, size_t smem) {
         set_error("exl3 moe: hipGetDevice failed");
         return -1;
     }
-    std::lock_guard<std::mutex> lock(mu);
-    for (int j = 0; j < ncache; ++j)
-        if (cache[j].fn == fn && cache[j].threads == threads && cache[j].smem == smem && cache[j].dev == dev)
-            return cache[j].grid;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-        set_error("exl3 moe: occupancy query failed");
-        return -1;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (int j = 0; j < ncache && !per_cu; ++j)
+            if (cache[j].fn == fn && cache[j].threads == threads && cache[j].smem == smem && cache[j].dev == dev) {
+                per_cu = cache[j].per_cu;
+                cus = cache[j].cus;
+            }
+        if (!per_cu) {
+            // Workgroups per CU from the kernel's own resources: 4 SIMDs x 512
+            // VGPRs (granule 8), at most 8 waves per SIMD, 160 KB of LDS.
+            hipFuncAttributes fa;
+            if (hipFuncGetAttributes(&fa, fn) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+                set_error("exl3 moe: kernel attribute query failed");
+                return -1;
+            }
+            const int vgprs = ((fa.numRegs > 0 ? fa.numRegs : 128) + 7) & ~7;
+            int waves_simd = 512 / vgprs;
+            if (waves_simd > 8) waves_simd = 8;
+            const int waves_wg = (threads + 63) / 64;
+            per_cu = (4 * waves_simd) / waves_wg;
+            const size_t lds = smem + fa.sharedSizeBytes;
+            if (lds > 0 && (int)(kMaxLds / lds) < per_cu) per_cu = (int)(kMaxLds / lds);
+            if (per_cu < 1) per_cu = 1;
+            if (cus < 1) cus = 1;
+            if (getenv("EXL3_MOE_DEBUG"))
+                fprintf(stderr, "exl3 moe grid: regs=%d static_lds=%zu dyn_lds=%zu threads=%d per_cu=%d cus=%d\n",
+                        fa.numRegs, (size_t)fa.sharedSizeBytes, smem, threads, per_cu, cus);
+            if (ncache < 64) cache[ncache++] = Entry{fn, threads, smem, dev, per_cu, cus};
+        }
     }
-    const int grid = (per_cu < 1 ? 1 : per_cu) * (cus < 1 ? 1 : cus);
-    if (ncache < 64) cache[ncache++] = Entry{fn, threads, smem, dev, grid};
-    return grid;
+    const int forced = env_int_once("EXL3_MOE_WG_PER_CU");  // tuning override
+    return (forced > 0 ? forced : per_cu) * cus;
 }
 
 namespace {
@@ -181,7 +207,7 @@ constexpr int kMoeMaxExperts = 4096;
 constexpr int kMoeMaxEntries = 8192;
 
 struct MoePlan {
-    int ns, kw, splits;
+    int ns, kw, splits, bpi;
 };
 
 int env_int(const char* name, int dflt) {
@@ -205,6 +231,9 @@ double expected_active(int tokens, int topk, int E) {
 // weight bytes; failing both, the best compromise.
 MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
     const int kslices = k / 16;
+    // two 8-wave workgroups per CU when the LDS allows it (the kernel's
+    // register budget is set for that)
+    const size_t lds_two = kMaxLds / 2 - 1024;
     const double target = env_int("EXL3_MOE_TARGET_WAVES", 3072);
     const double max_traffic = env_int("EXL3_MOE_MAX_PARTIAL_PCT", 15) / 100.0;
     const int f_steps = env_int("EXL3_MOE_NSTEPS", 0), f_kw = env_int("EXL3_MOE_KW", 0);
@@ -216,7 +245,7 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
         for (int ns = 16; ns >= 2; ns /= 2) {
             const int kts_wg = 4 * ns * kw;
             if (kts_wg % 8 || kslices % kts_wg) continue;
-            if (moe_smem_bytes(kts_wg, kw) > kMaxLds - 1024) continue;  // headroom for static LDS
+            if (moe_smem_bytes(kts_wg, kw) > lds_two) continue;
             if ((f_steps && ns != f_steps) || (f_kw && kw != f_kw)) continue;
             const int S = kslices / kts_wg;
             const double waves = units * cols * S * 4 * kw;
@@ -224,12 +253,31 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
             // 1 when both goals hold; otherwise the worse of the two ratios
             const double score = fmin(1.0, fmin(waves / target, traffic > 0 ? max_traffic / traffic : 1.0));
             if (score > best_score + 1e-9) {
-                best = MoePlan{ns, kw, S};
+                best = MoePlan{ns, kw, S, 1};
                 best_score = score;
             }
         }
     }
-    if (best.ns == 0) best = MoePlan{2, 1, kslices / 8};
+    if (best.ns == 0) best = MoePlan{2, 1, kslices / 8, 1};
+    // Column blocks per item: an item stages (and rotates) its rows once for
+    // all of its blocks.  With several rows per unit that staging is the
+    // larger cost, so group blocks as long as the items still fill the device
+    // twice over; with one row per unit keep one block per item (parallelism).
+    const double rows_per_unit = units > 0 ? fmin((double)MOE_UNIT_ROWS, entries / units) : 1.0;
+    const int nblk = n / 128;
+    const int f_bpi = env_int("EXL3_MOE_BPI", 0);
+    if (f_bpi > 0 && nblk % f_bpi == 0) {
+        best.bpi = f_bpi;
+    } else if (rows_per_unit >= 4.0) {
+        const double wg_target = 2.0 * 512;  // 2 workgroups x 256 CUs, twice over
+        for (int bpi = nblk; bpi >= 1; --bpi) {
+            if (nblk % bpi) continue;
+            if (units * (nblk / bpi) * nproj * best.splits >= wg_target || bpi == 1) {
+                best.bpi = bpi;
+                break;
+            }
+        }
+    }
     return best;
 }
 
@@ -330,6 +378,7 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     p.nproj = 2;
     p.splits = L.gu.splits;
     p.kw = L.gu.kw;
+    p.bx_per_item = L.gu.bpi;
     int rc;
     if (KG == KU) {
         p.proj_base = 0;
@@ -357,6 +406,7 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     p.proj_launch = 1;
     p.splits = L.dn.splits;
     p.kw = L.dn.kw;
+    p.bx_per_item = L.dn.bpi;
     rc = moe_launch(KD, cb, L.dn.ns, p, st);
     if (rc) return rc;
 
@@ -385,7 +435,7 @@ extern "C" int exl3_moe_plan(int tokens, int topk, int num_experts, int hidden, 
     const MoeLayout L = moe_layout(tokens, topk, num_experts, hidden, inter);
     const MoePlan* pls[2] = {&L.gu, &L.dn};
     for (int j = 0; j < 2; ++j) {
-        out[4 * j + 0] = MOE_UNIT_ROWS;
+        out[4 * j + 0] = pls[j]->bpi;
         out[4 * j + 1] = pls[j]->ns;
         out[4 * j + 2] = pls[j]->kw;
         out[4 * j + 3] = pls[j]->splits;

@@ -33,6 +33,7 @@ constexpr int MOE_GATE_UP = 0;
 constexpr int MOE_DOWN = 1;
 constexpr int MOE_ROUTE_THREADS = 1024;
 constexpr int MOE_UNIT_ROWS = 16;  // rows of a work unit: one MFMA row block
+constexpr int MV_PRE = 2;          // rotation blocks per wave whose activations are preloaded
 
 // A work unit: up to 16 rows of one expert, with the expert's weight
 // addresses resolved by the routing kernel (one dependent load for the GEMV
@@ -70,6 +71,7 @@ struct MoeParams {
     int proj_launch;   // projections this launch enumerates (1 or 2)
     int splits;        // S
     int kw;            // k waves per workgroup
+    int bx_per_item;   // column blocks one item covers (divides n/128)
     int mode;
 };
 
@@ -78,6 +80,15 @@ inline size_t moe_route_smem_bytes(int E, int entries) { return (size_t)(3 * E +
 // ------------------------------------------------------------ expert GEMVs
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+// Wave-uniform values read from memory by vector loads, moved to scalar
+// registers (they would otherwise occupy a VGPR per lane).
+__device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ const void* uniform_p(const void* p) {
+    const unsigned long long u = reinterpret_cast<unsigned long long>(p);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u), hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+    return reinterpret_cast<const void*>(((unsigned long long)hi << 32) | lo);
+}
 
 __device__ __forceinline__ __half2 ld_h2_ptr(const void* base, int idx) {
     return ld_h2(gptr(reinterpret_cast<const __half*>(base)) + idx);
@@ -91,15 +102,16 @@ __device__ __forceinline__ __half2 ld_h2_ptr(const void* base, int idx) {
 // fp32 partial rows; the last of nproj * S arrivals of (unit, column block)
 // runs the epilogue.
 template <int K, int CB, int NS>
-__global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
+__global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
     constexpr int ROWS = MOE_UNIT_ROWS;
     extern __shared__ __align__(16) unsigned char mv_smem[];
     __shared__ int is_last;
 
-    const int nunits = gptr(p.rt.counts)[1];
+    const int nunits = uniform_i(gptr(p.rt.counts)[1]);
     const int nblk_n = p.n >> 7;
+    const int BPI = p.bx_per_item, ngroups = nblk_n / BPI;
     const int S = p.splits, P = p.proj_launch;
-    const int per_unit = nblk_n * P * S;
+    const int per_unit = ngroups * P * S;
     const int total = nunits * per_unit;
     if ((int)blockIdx.x >= total) return;
 
@@ -126,28 +138,25 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
     for (int it = blockIdx.x; it < total; it += gridDim.x) {
         const int u = it / per_unit;
         int rem = it - u * per_unit;
-        const int bx = rem / (P * S);
-        rem -= bx * P * S;
+        const int bg = rem / (P * S);
+        rem -= bg * P * S;
         const int pl = rem / S, sidx = rem - pl * S;
         const int proj = p.proj_base + pl;
 
         const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
-        const int m = ud->nrows, crow0 = ud->crow0;
+        const int m = uniform_i(ud->nrows), crow0 = uniform_i(ud->crow0);
         const int pb = pre_rotated ? 6 : 3 * proj;
-        const uint32_t* trellis = reinterpret_cast<const uint32_t*>(ud->ptr[pb]);
-        const void* suh = ud->ptr[pb + 1];
-        // epilogue vectors, requested now so they are in registers at the end
-        const int c0 = bx * 128 + 2 * lane;
-        const __half2 ev0 = ld_h2_ptr(ud->ptr[pre_rotated ? 8 : 2], c0);  // svh of down / gate
-        __half2 ev1 = __half2{}, ev2 = __half2{};
-        if (!pre_rotated) {
-            ev1 = ld_h2_ptr(ud->ptr[5], c0);  // svh of up
-            ev2 = ld_h2_ptr(ud->ptr[7], c0);  // suh of down (its input rotation)
-        }
-
-        const int nt = bx * 8 + cw * 2 + (i >> 3);
+        const uint32_t* trellis = reinterpret_cast<const uint32_t*>(uniform_p(ud->ptr[pb]));
+        const void* suh = uniform_p(ud->ptr[pb + 1]);
+        const void* ev0p = uniform_p(ud->ptr[pre_rotated ? 8 : 2]);  // svh of down / gate
+        const void* ev1p = uniform_p(ud->ptr[5]);                    // svh of up
+        const void* ev2p = uniform_p(ud->ptr[7]);                    // suh of down (its input rotation)
         const int kt_wg0 = sidx * kts_wg;
         const int kt_w0 = kt_wg0 + kwi * 4 * nsteps;
+        const int bx0 = bg * BPI;
+        auto tiles = [&](int bx) {
+            return gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + bx * 8 + cw * 2 + (i >> 3)) * (8 * K) + K * q;
+        };
         if (it != (int)blockIdx.x) __syncthreads();  // the previous item is done with LDS
 
         auto x_row = [&](int row) -> const EXL3_GLOBAL __half* {
@@ -156,11 +165,12 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
             return gptr(p.x) + (size_t)(rows_g[crow0 + row] / p.topk) * k;
         };
 
-        // 1. activation loads (up to GV_PRE blocks per wave), then the weights
+        // 1. activation loads (up to GV_PRE blocks per wave), then the first
+        //    column block's weights
         const int nrot = m * nblk128;
-        __half2 xpre[GV_PRE], spre[GV_PRE];
+        __half2 xpre[MV_PRE], spre[MV_PRE];
 #pragma unroll
-        for (int j = 0; j < GV_PRE; ++j) {
+        for (int j = 0; j < MV_PRE; ++j) {
             const int b = wave + j * nwaves;
             if (b < nrot) {
                 const int row = b / nblk128, bb = b - row * nblk128;
@@ -170,12 +180,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
             }
         }
         uint32_t w[gv_depth<K>()][K];
-        const EXL3_GLOBAL uint32_t* tb =
-            gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + nt) * (8 * K) + K * q;
-        prime_weights<K, NS>(w, tb, step_stride);
+        prime_weights<K, NS>(w, tiles(bx0), step_stride);
 
-        // 2. stage the rows in A-fragment order (rotated here unless they
-        //    arrive rotated)
+        // 2. stage the rows in A-fragment order once for all column blocks of
+        //    the item (rotated here unless they arrive rotated)
         auto stage = [&](int b, __half2 xv, __half2 sv) {
             const int row = b / nblk128, bb = b - row * nblk128;
             const int kk = bb * 128 + 2 * lane;
@@ -201,11 +209,11 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
             }
         };
 #pragma unroll
-        for (int j = 0; j < GV_PRE; ++j) {
+        for (int j = 0; j < MV_PRE; ++j) {
             const int b = wave + j * nwaves;
             if (b < nrot) stage(b, xpre[j], spre[j]);
         }
-        for (int b = wave + GV_PRE * nwaves; b < nrot; b += nwaves) {
+        for (int b = wave + MV_PRE * nwaves; b < nrot; b += nwaves) {
             const int row = b / nblk128, bb = b - row * nblk128;
             const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
             const __half2 sv = pre_rotated ? __half2{} : ld_h2_ptr(suh, kg);
@@ -213,99 +221,132 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void moe_gemv_kernel(MoeParams p) {
         }
         __syncthreads();
 
-        // 3. decode + MFMA (rows >= m read nothing and multiply zeros)
-        float4_t acc[1][2];
-        acc[0][0] = float4_t{0.f, 0.f, 0.f, 0.f};
-        acc[0][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         const bool live = i < m;
         const _Float16* a_base[1] = {xs + (size_t)((live ? i : 0) * kts_wg + kwi * 4 * nsteps + g) * 4 * 8};
         const bool a_live[1] = {live};
-        decode_mfma_steps<K, CB, 1, NS>(w, tb, step_stride, a_base, a_live, acc);
+        for (int bx = bx0; bx < bx0 + BPI; ++bx) {
+            if (bx != bx0) {
+                __syncthreads();  // the previous block is done with ybuf
+                prime_weights<K, NS>(w, tiles(bx), step_stride);
+            }
+            // epilogue vectors of this block, requested now so they are in
+            // registers at the end
+            const int c0 = bx * 128 + 2 * lane;
+            const __half2 ev0 = ld_h2_ptr(ev0p, c0);
+            __half2 ev1 = __half2{}, ev2 = __half2{};
+            if (!pre_rotated) {
+                ev1 = ld_h2_ptr(ev1p, c0);
+                ev2 = ld_h2_ptr(ev2p, c0);
+            }
 
-        // 4. k waves summed through LDS, mul1 affine map, partial rows out
+            // 3. decode + MFMA (rows >= m read nothing and multiply zeros)
+            float4_t acc[1][2];
+            acc[0][0] = float4_t{0.f, 0.f, 0.f, 0.f};
+            acc[0][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+            decode_mfma_steps<K, CB, 1, NS>(w, tiles(bx), step_stride, a_base, a_live, acc);
+
+            // 4. k waves summed through LDS, mul1 affine map, partial rows out
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 4 * g + r;
-                const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                if (row < m) ybuf[(kwi * ROWS + row) * 128 + col] = acc[0][c][r];
-            }
-        __syncthreads();
-        float* part = p.partials + ((size_t)(bx * p.nproj + proj) * S + sidx) * split_stride + (size_t)crow0 * 128;
-        for (int idx = tid; idx < m * 128; idx += nthreads) {
-            float v = ybuf[idx];
-            for (int j = 1; j < kw; ++j) v += ybuf[j * ROWS * 128 + idx];
-            if constexpr (CB == 2) {
-                const int row = idx >> 7;
-                float sx = 0.f;
-                for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
-                v = v * kMul1Kinv + kMul1Delta * sx;
-            }
-            coherent_store(part + idx, v);
-        }
-
-        // 5. hand-off: the last of nproj * S arrivals for (unit, column block) finishes
-        wait_stores();
-        __syncthreads();
-        int* ctr = p.counters + (size_t)u * nblk_n + bx;
-        if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            is_last = (old == p.nproj * S - 1);
-        }
-        __syncthreads();
-        if (!is_last) continue;
-        if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-        // 6. epilogue, one row per wave, 2 columns per lane
-        auto sum_proj = [&](int pj, int crow, float& va, float& vb) {
-            const float* base =
-                p.partials + (size_t)(bx * p.nproj + pj) * S * split_stride + (size_t)crow * 128 + 2 * lane;
-            va = 0.f;
-            vb = 0.f;
-            for (int s2 = 0; s2 < S; ++s2) {
-                va += coherent_load(base + s2 * split_stride);
-                vb += coherent_load(base + s2 * split_stride + 1);
-            }
-        };
-        EXL3_GLOBAL __half* outg = gptr(p.out);
-        if (!pre_rotated) {
-            const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
-            for (int row = wave; row < m; row += nwaves) {
-                const int crow = crow0 + row;
-                float ga, gb, ua, ub;
-                sum_proj(0, crow, ga, gb);
-                sum_proj(1, crow, ua, ub);
-                fwht128_pair_f(ga, gb, lane);
-                fwht128_pair_f(ua, ub, lane);
-                // gate and up outputs in fp16, as the separate linears return them
-                const __half2 gh =
-                    __floats2half2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
-                const __half2 uh =
-                    __floats2half2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
-                float g0 = __low2float(gh), g1 = __high2float(gh), u0 = __low2float(uh), u1 = __high2float(uh);
-                if (clamp) {
-                    g0 = fminf(g0, p.limit);
-                    g1 = fminf(g1, p.limit);
-                    u0 = fminf(fmaxf(u0, -p.limit), p.limit);
-                    u1 = fminf(fmaxf(u1, -p.limit), p.limit);
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 4 * g + r;
+                    const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                    if (row < m) ybuf[(kwi * ROWS + row) * 128 + col] = acc[0][c][r];
                 }
-                const __half2 act = __floats2half2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
-                // input rotation of the down projection for this 128-wide chunk
-                const __half2 pr = __hmul2(act, ev2);
-                float da = __low2float(pr), db = __high2float(pr);
-                fwht128_pair_f(da, db, lane);
-                st_h2(outg + (size_t)crow * n + c0, __floats2half2_rn(da * kHadNorm, db * kHadNorm));
+            __syncthreads();
+            float* part =
+                p.partials + ((size_t)(bx * p.nproj + proj) * S + sidx) * split_stride + (size_t)crow0 * 128;
+            for (int idx = tid; idx < m * 128; idx += nthreads) {
+                float v = ybuf[idx];
+                for (int j = 1; j < kw; ++j) v += ybuf[j * ROWS * 128 + idx];
+                if constexpr (CB == 2) {
+                    const int row = idx >> 7;
+                    float sx = 0.f;
+                    for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+                    v = v * kMul1Kinv + kMul1Delta * sx;
+                }
+                coherent_store(part + idx, v);
             }
-        } else {
-            for (int row = wave; row < m; row += nwaves) {
-                const int crow = crow0 + row;
-                float va, vb;
-                sum_proj(0, crow, va, vb);
-                fwht128_pair_f(va, vb, lane);
-                const int entry = rows_g[crow];
-                st_h2(outg + (size_t)entry * n + c0,
-                      __floats2half2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0)));
+
+            // 5. hand-off: the last of nproj * S arrivals for (unit, column
+            //    block) finishes
+            wait_stores();
+            __syncthreads();
+            int* ctr = p.counters + (size_t)u * nblk_n + bx;
+            if (tid == 0) {
+                const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                is_last = (old == p.nproj * S - 1);
+            }
+            __syncthreads();
+            if (!is_last) continue;
+            if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+            // 6. epilogue, one row per wave, 2 columns per lane; split partials
+            //    of a row are all requested before the first add (one round
+            //    trip) and summed in split order
+            auto sum_rows = [&](int np, int crow, float2* out) {
+                constexpr int G = 8;
+                for (int s0 = 0; s0 < S; s0 += G) {
+                    float2 v[2][G];
+#pragma unroll
+                    for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+                        for (int j = 0; j < G; ++j)
+                            if (pj < np && s0 + j < S)
+                                v[pj][j] = coherent_load2(
+                                    p.partials + ((size_t)(bx * p.nproj + pj) * S + s0 + j) * split_stride +
+                                    (size_t)crow * 128 + 2 * lane);
+#pragma unroll
+                    for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+                        for (int j = 0; j < G; ++j)
+                            if (pj < np && s0 + j < S) {
+                                out[pj].x += v[pj][j].x;
+                                out[pj].y += v[pj][j].y;
+                            }
+                }
+            };
+            EXL3_GLOBAL __half* outg = gptr(p.out);
+            if (!pre_rotated) {
+                const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
+                for (int row = wave; row < m; row += nwaves) {
+                    const int crow = crow0 + row;
+                    float2 gu[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+                    sum_rows(2, crow, gu);
+                    float ga = gu[0].x, gb = gu[0].y, ua = gu[1].x, ub = gu[1].y;
+                    fwht128_pair_f(ga, gb, lane);
+                    fwht128_pair_f(ua, ub, lane);
+                    // gate and up outputs in fp16, as the separate linears return them
+                    const __half2 gh =
+                        __floats2half2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
+                    const __half2 uh =
+                        __floats2half2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
+                    float g0 = __low2float(gh), g1 = __high2float(gh), u0 = __low2float(uh), u1 = __high2float(uh);
+                    if (clamp) {
+                        g0 = fminf(g0, p.limit);
+                        g1 = fminf(g1, p.limit);
+                        u0 = fminf(fmaxf(u0, -p.limit), p.limit);
+                        u1 = fminf(fmaxf(u1, -p.limit), p.limit);
+                    }
+                    const __half2 act = __floats2half2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
+                    // input rotation of the down projection for this 128-wide chunk
+                    const __half2 pr = __hmul2(act, ev2);
+                    float da = __low2float(pr), db = __high2float(pr);
+                    fwht128_pair_f(da, db, lane);
+                    st_h2(outg + (size_t)crow * n + c0, __floats2half2_rn(da * kHadNorm, db * kHadNorm));
+                }
+            } else {
+                for (int row = wave; row < m; row += nwaves) {
+                    const int crow = crow0 + row;
+                    float2 d[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+                    sum_rows(1, crow, d);
+                    float va = d[0].x, vb = d[0].y;
+                    fwht128_pair_f(va, vb, lane);
+                    const int entry = rows_g[crow];
+                    st_h2(outg + (size_t)entry * n + c0,
+                          __floats2half2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0)));
+                }
             }
         }
     }

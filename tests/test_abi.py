@@ -101,8 +101,8 @@ def test_moe_plan_and_workspace_are_host_only():
         assert L.exl3_moe_plan(T, 8, 128, 2048, 768, out) == 0
         gu, dn, units = list(out)[:4], list(out)[4:8], out[8]
         assert units == min(128, 8 * T) + (8 * T + 15) // 16  # bound on 16-row work units
-        for (rows, ns, kw, S), k in ((gu, 2048), (dn, 768)):
-            assert rows == 16
+        for (bpi, ns, kw, S), k, n in ((gu, 2048, 768), (dn, 768, 2048)):
+            assert (n // 128) % bpi == 0
             assert 4 * ns * kw * S == k // 16
         assert L.exl3_moe_workspace_size(T, 8, 128, 2048, 768) > 256 * 1024
     assert L.exl3_moe_workspace_size(0, 8, 128, 2048, 768) == 0
