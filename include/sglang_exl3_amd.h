@@ -100,12 +100,37 @@ int exl3_gemv(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, co
               uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
               size_t workspace_bytes, void* stream);
 
-/* Same product for any number of rows m >= 1 (prefill).
+/* Same product for any number of rows m >= 1: up to 64 rows the GEMV kernel;
+ * above, the input is rotated once and the MFMA GEMM (exl3_fat_gemm's
+ * kernel) runs over it (workspace: exl3_gemm_workspace_size).
  * Replaces exl3_gemm (csrc/bindings.cpp:110-115 -> csrc/exl3_gemm.cu:9-31;
  * torch op sglang_exl3::exl3_gemm, src/sglang_exl3/ops.py:77-93). */
 int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
               uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
               size_t workspace_bytes, void* stream);
+
+/* Scratch bytes exl3_gemm needs for m rows: the GEMV workspace for m <= 64,
+ * above that the prefill scratch (rotated input m*k fp16 + m*n fp32).  The
+ * workspace must start zero-filled (counters), as for exl3_gemv. */
+size_t exl3_gemm_workspace_size(int m, int k, int n, int K);
+
+/* Many-row EXL3 GEMM on MFMA with the input already rotated:
+ *   out[m][n] (f32) = svh[n] * (H . (a . T)[m][128-block])[n] / sqrt(128)
+ * a: f16 [M][k] = fp16(H(x (.) suh) / sqrt(128)) per 128 block; trellis
+ * [k/16][n/16][16K]; any K in 1..8 and codebook (the reference: K = 4 MCG
+ * only).  `out` is overwritten.
+ * Replaces exl3_fat_gemm (csrc/exl3_fat_gemm.cu:275-287; torch op
+ * sglang_exl3::exl3_fat_gemm, src/sglang_exl3/ops.py:187-204). */
+int exl3_fat_gemm(const uint16_t* a, const int16_t* trellis, float* out, const uint16_t* svh, int M, int k, int n,
+                  int K, int codebook, void* stream);
+
+/* As exl3_fat_gemm, but row m is scaled by route_weight[m] (f16) and added
+ * into out[token_idx[m]] (int64), atomically (rows may share a destination).
+ * Replaces exl3_fat_gemm_scatter (csrc/exl3_fat_gemm.cu:289-305; torch op
+ * sglang_exl3::exl3_fat_gemm_scatter, src/sglang_exl3/ops.py:207-226). */
+int exl3_fat_gemm_scatter(const uint16_t* a, const int16_t* trellis, float* out, const uint16_t* svh,
+                          const int64_t* token_idx, const uint16_t* route_weight, int M, int k, int n, int K,
+                          int codebook, void* stream);
 
 /* For each active slot e < num_active: out[e] (f16 [m][n]) = x_e . W_{ids[e]}
  * where x_e = x (x_per_expert == 0, x is [m][k]) or x + e*m*k (x_per_expert

@@ -1,0 +1,189 @@
+// C ABI of the many-row EXL3 GEMM: exl3_fat_gemm, exl3_fat_gemm_scatter and
+// the prefill path of exl3_gemm (rotate -> fat GEMM -> fp16), with the launch
+// planner (rows per tile, k-splits).
+#include "exl3_fat_impl.h"
+
+namespace exl3 {
+
+int fat_launch_K1(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K2(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K3(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K4(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K5(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K6(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K7(int, int, const FatParams&, int, hipStream_t);
+int fat_launch_K8(int, int, const FatParams&, int, hipStream_t);
+
+int fat_launch(int K, int cb, int mt, const FatParams& p, int splits, hipStream_t st) {
+    switch (K) {
+        case 1: return fat_launch_K1(cb, mt, p, splits, st);
+        case 2: return fat_launch_K2(cb, mt, p, splits, st);
+        case 3: return fat_launch_K3(cb, mt, p, splits, st);
+        case 4: return fat_launch_K4(cb, mt, p, splits, st);
+        case 5: return fat_launch_K5(cb, mt, p, splits, st);
+        case 6: return fat_launch_K6(cb, mt, p, splits, st);
+        case 7: return fat_launch_K7(cb, mt, p, splits, st);
+        case 8: return fat_launch_K8(cb, mt, p, splits, st);
+    }
+    set_error("exl3 fat gemm: K=%d outside 1..8", K);
+    return EXL3_ERR_UNSUPPORTED;
+}
+
+namespace {
+
+__global__ void fill_f32_kernel(float* p, size_t n, float v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void f32_to_f16_kernel(const float* src, __half* dst, size_t n2) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n2; i += (size_t)gridDim.x * blockDim.x) {
+        const float2 v = reinterpret_cast<const float2*>(src)[i];
+        reinterpret_cast<__half2*>(dst)[i] = __floats2half2_rn(v.x, v.y);
+    }
+}
+
+// Input rotation of the prefill path: xr = fp16( H(x (.) suh) / sqrt(128) ), one wave per 128 chunk.
+__global__ __launch_bounds__(256) void rotate_rows_kernel(const __half* x, const __half* suh, __half* xr,
+                                                          long long chunks, int k) {
+    const long long chunk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (chunk >= chunks) return;
+    const int lane = threadIdx.x & 63, per_row = k >> 7;
+    const long long row = chunk / per_row;
+    const int c = (int)(chunk - row * per_row) * 128 + 2 * lane;
+    const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)row * k + c), ld_h2(gptr(suh) + c));
+    float a = __low2float(pr), b = __high2float(pr);
+    fwht128_pair_f(a, b, lane);
+    st_h2(gptr(xr) + (size_t)row * k + c, __floats2half2_rn(a * kHadNorm, b * kHadNorm));
+}
+
+struct FatPlan {
+    int mt, splits;
+};
+
+// Rows per tile from M; k-splits until the grid holds ~4 workgroups per CU
+// (each split's steps must be whole chunks of FAT_CH, except a lone tail).
+FatPlan plan_fat(int M, int k, int n) {
+    FatPlan pl;
+    pl.mt = M >= 128 ? 128 : (M > 16 ? 64 : 16);
+    const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
+    const int ksteps = k / 64;
+    pl.splits = 1;
+    while (base * pl.splits < 1024 && pl.splits < 16 && ksteps % (2 * pl.splits) == 0 &&
+           (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+        pl.splits *= 2;
+    return pl;
+}
+
+int check_fat(const char* fn, const void* a, const void* trellis, const void* out, const void* svh, int M, int k,
+              int n, int K, int cb) {
+    EXL3_REQUIRE(M >= 0, "%s: M=%d", fn, M);
+    EXL3_REQUIRE(k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0, "%s: k=%d n=%d must be positive multiples of 128",
+                 fn, k, n);
+    EXL3_REQUIRE(K >= 1 && K <= 8, "%s: K=%d outside 1..8", fn, K);
+    EXL3_REQUIRE(cb >= 0 && cb <= 2, "%s: codebook=%d outside 0..2", fn, cb);
+    EXL3_REQUIRE(M == 0 || (a && trellis && out && svh), "%s: null pointer", fn);
+    EXL3_REQUIRE(aligned(a, 16) && aligned(trellis, 16) && aligned(out, 8) && aligned(svh, 4),
+                 "%s: misaligned pointer", fn);
+    return EXL3_OK;
+}
+
+int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out16, const uint16_t* svh,
+            const int64_t* token_idx, const uint16_t* route_w, int M, int k, int n, int K, int cb, bool zero_first,
+            hipStream_t st) {
+    const FatPlan pl = plan_fat(M, k, n);
+    FatParams p{};
+    p.a = reinterpret_cast<const __half*>(a);
+    p.trellis = reinterpret_cast<const uint32_t*>(trellis);
+    p.svh = reinterpret_cast<const __half*>(svh);
+    p.out32 = out32;
+    p.out16 = out16;
+    p.token_idx = token_idx;
+    p.route_w = reinterpret_cast<const __half*>(route_w);
+    p.M = M;
+    p.k = k;
+    p.n = n;
+    p.ksteps = k / 64 / pl.splits;
+    const bool scatter = token_idx != nullptr;
+    p.accumulate = (scatter || pl.splits > 1) ? 1 : 0;
+    if (out16 && p.accumulate) {
+        set_error("exl3 fat gemm: fp16 output needs a single k-split");
+        return EXL3_ERR_UNSUPPORTED;
+    }
+    if (zero_first && p.accumulate && !scatter) {
+        const size_t cnt = (size_t)M * n;
+        fill_f32_kernel<<<(unsigned)((cnt + 255) / 256 < 4096 ? (cnt + 255) / 256 : 4096), 256, 0, st>>>(out32, cnt,
+                                                                                                       0.f);
+        const int rc = launch_status("exl3 fat gemm zero fill");
+        if (rc) return rc;
+    }
+    return fat_launch(K, cb, pl.mt, p, pl.splits, st);
+}
+
+}  // namespace
+
+// Prefill path of exl3_gemm (m > 64).  Scratch after the workspace's counter
+// region (shared with the GEMV kernels, which need it to stay zero):
+// [counters][xr fp16 m*k][out fp32 m*n].
+size_t fat_xr_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
+size_t fat_gemm_scratch_bytes(int m, int k, int n) {
+    return kWsCounterBytes + fat_xr_bytes(m, k) + (size_t)m * n * 4;
+}
+
+int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,
+                  int m, int k, int n, int K, int cb, void* ws, size_t ws_bytes, hipStream_t st) {
+    const size_t need = fat_gemm_scratch_bytes(m, k, n);
+    EXL3_REQUIRE_CODE(ws && ws_bytes >= need, EXL3_ERR_WORKSPACE,
+                      "exl3_gemm: %zu workspace bytes needed for m=%d, %zu given", need, m,
+                      ws ? ws_bytes : (size_t)0);
+    EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4), "exl3_gemm: misaligned pointer");
+    __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsCounterBytes);
+    float* o32 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsCounterBytes + fat_xr_bytes(m, k));
+    const long long chunks = (long long)m * (k / 128);
+    rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x),
+                                                                      reinterpret_cast<const __half*>(suh), xr, chunks,
+                                                                      k);
+    int rc = launch_status("exl3_gemm rotate launch");
+    if (rc) return rc;
+    const FatPlan pl = plan_fat(m, k, n);
+    if (pl.splits == 1) {
+        return run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, nullptr, reinterpret_cast<__half*>(y), svh,
+                       nullptr, nullptr, m, k, n, K, cb, false, st);
+    }
+    rc = run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, o32, nullptr, svh, nullptr, nullptr, m, k, n, K, cb,
+                 true, st);
+    if (rc) return rc;
+    const size_t n2 = (size_t)m * n / 2;
+    f32_to_f16_kernel<<<(unsigned)((n2 + 255) / 256 < 8192 ? (n2 + 255) / 256 : 8192), 256, 0, st>>>(
+        o32, reinterpret_cast<__half*>(y), n2);
+    return launch_status("exl3_gemm convert launch");
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_fat_gemm(const uint16_t* a, const int16_t* trellis, float* out, const uint16_t* svh, int M, int k,
+                             int n, int K, int codebook, void* stream) {
+    clear_error();
+    int rc = check_fat("exl3_fat_gemm", a, trellis, out, svh, M, k, n, K, codebook);
+    if (rc || M == 0) return rc;
+    return run_fat(a, trellis, out, nullptr, svh, nullptr, nullptr, M, k, n, K, codebook, true, as_stream(stream));
+}
+
+extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, const int16_t* trellis, float* out, const uint16_t* svh,
+                                     const int64_t* token_idx, const uint16_t* route_weight, int M, int k, int n,
+                                     int K, int codebook, void* stream) {
+    clear_error();
+    int rc = check_fat("exl3_fat_gemm_scatter", a, trellis, out, svh, M, k, n, K, codebook);
+    if (rc || M == 0) return rc;
+    EXL3_REQUIRE(token_idx && route_weight, "exl3_fat_gemm_scatter: null routing pointer");
+    return run_fat(a, trellis, out, nullptr, svh, token_idx, route_weight, M, k, n, K, codebook, false,
+                   as_stream(stream));
+}
+
+extern "C" size_t exl3_gemm_workspace_size(int m, int k, int n, int K) {
+    if (m < 1 || k < 128 || n < 128) return 0;
+    if (m <= 64) return exl3_gemv_workspace_size(m, k, n, K, 1);
+    return fat_gemm_scratch_bytes(m, k, n);
+}

@@ -32,6 +32,9 @@ int gemv_launch(int K, int cb, int mb, const GemvParams& p, int experts, hipStre
     return EXL3_ERR_UNSUPPORTED;
 }
 
+int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,
+                  int m, int k, int n, int K, int cb, void* ws, size_t ws_bytes, hipStream_t st);
+
 namespace {
 
 constexpr int kMaxGemvRows = 64;
@@ -191,6 +194,8 @@ extern "C" int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16
     EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4) && aligned(svh, 4) && aligned(trellis, 16),
                  "exl3_gemm: misaligned pointer");
     hipStream_t st = as_stream(stream);
+    if (m > kMaxGemvRows) return fat_gemm_rows(x, trellis, suh, svh, y, m, k, n, K, codebook, workspace,
+                                               workspace_bytes, st);
     for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
         const int mc = (m - r0) < kMaxGemvRows ? (m - r0) : kMaxGemvRows;
         GemvParams p = base_params(x + (size_t)r0 * k, trellis, suh, svh, y + (size_t)r0 * n, mc, k, n);

@@ -50,7 +50,7 @@ def linear_forward(x2: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, s
         return y
     L = _lib.lib()
     with torch.cuda.device(x2.device):
-        need = int(L.exl3_gemv_workspace_size(min(rows, 64), k, n, int(K), 1))
+        need = int(L.exl3_gemm_workspace_size(rows, k, n, int(K)))
         ws = workspace(x2.device, need) if need else None
         fn = L.exl3_gemv if rows <= 64 else L.exl3_gemm
         rc = fn(x2.data_ptr(), trellis.data_ptr(), suh.data_ptr(), svh.data_ptr(), y.data_ptr(), rows, k, n, int(K),

@@ -119,7 +119,7 @@ def _gemv_like(name, fn, x, trellis, suh, svh, K, mcg, max_rows=None):
     y = torch.empty((m, n), dtype=torch.float16, device=x.device)
     lib = _lib.lib()
     with torch.cuda.device(x.device):
-        need = int(lib.exl3_gemv_workspace_size(min(m, 64), kdim, n, int(K), 1))
+        need = int(lib.exl3_gemm_workspace_size(m, kdim, n, int(K)))
         ws = workspace(x.device, need) if need else None
         rc = fn(x2.data_ptr(), tr.data_ptr(), suh.data_ptr(), svh.data_ptr(), y.data_ptr(), m, kdim, n,
                 int(K), _lib.codebook_from_mcg(bool(mcg)), 0 if ws is None else ws.data_ptr(),
@@ -264,14 +264,53 @@ def exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_p
     return out
 
 
-def _not_built(name):
-    def _fn(*args, **kwargs):
-        raise RuntimeError(f"sglang_exl3::{name} is not implemented in this build")
-    return _fn
+def _fat_common(name, a, packed, out, svh, K):
+    _require_device(name, a, packed, out, svh)
+    if a.dtype != torch.float16 or a.dim() != 2 or not a.is_contiguous():
+        raise RuntimeError(f"sglang_exl3::{name}: a must be a contiguous fp16 [M, k] tensor")
+    _check_trellis(name, packed, K)
+    if not packed.is_contiguous() or not svh.is_contiguous() or not out.is_contiguous():
+        raise RuntimeError(f"sglang_exl3::{name}: tensors must be contiguous")
+    if out.dtype != torch.float32 or out.dim() != 2:
+        raise RuntimeError(f"sglang_exl3::{name}: out must be float32 [rows, N]")
+    if svh.dtype != torch.float16 or svh.dim() != 1:
+        raise RuntimeError(f"sglang_exl3::{name}: svh must be a float16 vector")
+    M, k = int(a.shape[0]), int(a.shape[1])
+    n = int(svh.numel())
+    if k != int(packed.shape[0]) * 16 or n != int(packed.shape[1]) * 16:
+        raise RuntimeError(f"sglang_exl3::{name}: a / svh do not match the packed tensor")
+    if int(out.shape[1]) != n:
+        raise RuntimeError(f"sglang_exl3::{name}: out N dimension mismatch")
+    return M, k, n
 
 
-exl3_fat_gemm_impl = _not_built("exl3_fat_gemm")
-exl3_fat_gemm_scatter_impl = _not_built("exl3_fat_gemm_scatter")
+def exl3_fat_gemm_impl(a, packed, out, svh, K, mcg, mul1):
+    """out (fp32 [M, N]) = svh * H(a . T) / sqrt(128), a rotated (csrc/exl3_fat_gemm.cu:275-287)."""
+    name = "exl3_fat_gemm"
+    M, k, n = _fat_common(name, a, packed, out, svh, K)
+    if tuple(out.shape) != (M, n):
+        raise RuntimeError(f"sglang_exl3::{name}: out shape must be [M, N]")
+    with torch.cuda.device(a.device):
+        rc = _lib.lib().exl3_fat_gemm(a.data_ptr(), packed.data_ptr(), out.data_ptr(), svh.data_ptr(), M, k, n,
+                                      int(K), _lib.codebook_id(bool(mcg), bool(mul1)), _stream_ptr(a))
+    _lib.check(rc, name)
+
+
+def exl3_fat_gemm_scatter_impl(a, packed, out, svh, token_idx, route_weight, K, mcg, mul1):
+    """out[token_idx[m]] += route_weight[m] * (svh * H(a . T)[m] / sqrt(128)) (csrc/exl3_fat_gemm.cu:289-305)."""
+    name = "exl3_fat_gemm_scatter"
+    M, k, n = _fat_common(name, a, packed, out, svh, K)
+    _require_device(name, a, token_idx, route_weight)
+    if token_idx.dtype != torch.int64 or route_weight.dtype != torch.float16:
+        raise RuntimeError(f"sglang_exl3::{name}: token_idx must be int64 and route_weight float16")
+    if token_idx.numel() != M or route_weight.numel() != M:
+        raise RuntimeError(f"sglang_exl3::{name}: routing tensors must have M elements")
+    ti, rw = token_idx.contiguous(), route_weight.contiguous()
+    with torch.cuda.device(a.device):
+        rc = _lib.lib().exl3_fat_gemm_scatter(a.data_ptr(), packed.data_ptr(), out.data_ptr(), svh.data_ptr(),
+                                              ti.data_ptr(), rw.data_ptr(), M, k, n, int(K),
+                                              _lib.codebook_id(bool(mcg), bool(mul1)), _stream_ptr(a))
+    _lib.check(rc, name)
 
 
 # ----------------------------------------------------------------- registry

@@ -1,0 +1,101 @@
+"""GPU parity of the many-row MFMA GEMM: exl3_fat_gemm / exl3_fat_gemm_scatter
+(rotated fp16 input, fp32 output) and exl3_gemm's prefill path (m > 64),
+against the oracle (bar: max-abs-err <= 2e-2 * rms(ref), cosine >= 0.9999)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import check_close, make_weight, make_x
+from sglang_exl3 import ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _registered():
+    ops.register_custom_ops()
+
+
+def _rotate(x, suh):
+    """fp16(H(x * suh) / sqrt(128)) per 128 block (the input the fat GEMM takes)."""
+    return oracle.had_rows(x.astype(np.float32), suh, None, np.float32(0.08838834764831845)).astype(np.float16)
+
+
+def _ref(a_rot, trellis, svh, K, cb):
+    """svh * H(a_rot . T) / sqrt(128), with T the decoded tiles (no rotations)."""
+    k, n = trellis.shape[0] * 16, trellis.shape[1] * 16
+    ones_k = np.ones(k, dtype=np.float16)
+    ones_n = np.ones(n, dtype=np.float16)
+    # the oracle's dequant W = suh*svh*(H T H)/128; with unit scales, H W H = 128 T... use decode_tile directly
+    T = np.zeros((k, n), dtype=np.float32)
+    for kt in range(k // 16):
+        for nt in range(n // 16):
+            T[kt * 16:(kt + 1) * 16, nt * 16:(nt + 1) * 16] = oracle.f16_to_f32(
+                oracle.decode_tile(trellis[kt, nt].view(np.uint16), K, cb, rtz=False))
+    y = a_rot.astype(np.float64) @ T.astype(np.float64)
+    del ones_k, ones_n
+    return oracle.had_rows(y.astype(np.float32), None, svh, np.float32(0.08838834764831845))
+
+
+@pytest.mark.parametrize("M,k,n,K,cb", [
+    (16, 256, 256, 4, 1), (1, 256, 128, 3, 2), (40, 512, 384, 3, 1), (128, 256, 256, 4, 0),
+    (200, 1024, 256, 2, 2), (300, 256, 512, 5, 1),
+])
+def test_fat_gemm_vs_oracle(M, k, n, K, cb):
+    print(f"case: fat M={M} k={k} n={n} K={K} cb={cb}", flush=True)
+    tr, su, sv = make_weight(k, n, K, seed=M * 13 + K)
+    x = make_x(M, k, seed=M)
+    a = _rotate(x, su)
+    out = torch.full((M, n), 123.0, dtype=torch.float32, device="cuda")  # overwritten
+    mcg, mul1 = cb == 1, cb == 2
+    torch.ops.sglang_exl3.exl3_fat_gemm(torch.from_numpy(a).cuda(), torch.from_numpy(tr).cuda(), out,
+                                        torch.from_numpy(sv).cuda(), K, mcg, mul1)
+    torch.cuda.synchronize()
+    check_close(out.cpu().numpy(), _ref(a, tr, sv, K, cb), f"fat M={M}")
+
+
+def test_fat_gemm_scatter_accumulates():
+    M, k, n, K = 48, 256, 256, 4
+    tr, su, sv = make_weight(k, n, K, seed=5)
+    x = make_x(M, k, seed=6)
+    a = _rotate(x, su)
+    rng = np.random.default_rng(7)
+    tok = rng.integers(0, 20, size=M).astype(np.int64)  # destinations repeat: atomics
+    rw = (rng.random(M) + 0.5).astype(np.float16)
+    base = rng.standard_normal((20, n)).astype(np.float32)
+    out = torch.from_numpy(base.copy()).cuda()
+    torch.ops.sglang_exl3.exl3_fat_gemm_scatter(torch.from_numpy(a).cuda(), torch.from_numpy(tr).cuda(), out,
+                                                torch.from_numpy(sv).cuda(), torch.from_numpy(tok).cuda(),
+                                                torch.from_numpy(rw).cuda(), K, True, False)
+    torch.cuda.synchronize()
+    rows = _ref(a, tr, sv, K, 1) * rw.astype(np.float32)[:, None]
+    want = base.copy()
+    np.add.at(want, tok, rows)
+    check_close(out.cpu().numpy() - base, want - base, "fat scatter")
+
+
+@pytest.mark.parametrize("m,k,n,K,cb", [(65, 256, 256, 4, 1), (200, 512, 384, 3, 2), (1000, 256, 128, 2, 1)])
+def test_gemm_prefill_path_vs_oracle(m, k, n, K, cb):
+    print(f"case: gemm prefill m={m} k={k} n={n}", flush=True)
+    tr, su, sv = make_weight(k, n, K, seed=m + k)
+    x = make_x(m, k, seed=m)
+    y = torch.ops.sglang_exl3.exl3_gemm(torch.from_numpy(x).cuda(), torch.from_numpy(tr).cuda(),
+                                        torch.from_numpy(su).cuda(), torch.from_numpy(sv).cuda(), K, cb == 1)
+    torch.cuda.synchronize()
+    ref = oracle.matmul(x, oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    check_close(y.float().cpu().numpy(), ref, f"gemm prefill m={m}")
+
+
+def test_fat_then_gemv_workspace_stays_clean():
+    """The prefill scratch must not disturb the GEMV counters sharing the workspace."""
+    k, n, K = 512, 1024, 4
+    tr, su, sv = make_weight(k, n, K, seed=1)
+    d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
+    xb = make_x(300, k, seed=2)
+    torch.ops.sglang_exl3.exl3_gemm(torch.from_numpy(xb).cuda(), *d, K, True)
+    xs = make_x(2, k, seed=3)
+    y = torch.ops.sglang_exl3.exl3_gemv(torch.from_numpy(xs).cuda(), *d, K, True, 1)
+    torch.cuda.synchronize()
+    check_close(y.float().cpu().numpy(), oracle.matmul(xs, oracle.dequant(tr, su, sv, K, 1, rtz=True)), "gemv after")
