@@ -223,6 +223,117 @@ def moe_bench(torch, steps):
     return res
 
 
+# -------------------------------------------------------- fat gate+up (config 3)
+
+FAT_K, FAT_N, FAT_BITS, FAT_COPIES = 4096, 2 * 14336, 3, 8  # 8 x 44 MB > the Infinity Cache
+
+
+def fat_bench(torch, L):
+    """exl3_fat_gemm over the concatenated gate|up weight (mul1, K=3): rotated
+    fp16 input, fp32 output; M=16 (HBM-bound) and M=2048 (MFMA-bound)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(31)
+    trs = [torch.randint(-32768, 32768, (FAT_K // 16, FAT_N // 16, 16 * FAT_BITS), dtype=torch.int16, device="cuda",
+                         generator=g) for _ in range(FAT_COPIES)]
+    svh = ((torch.randint(0, 2, (FAT_N,), device="cuda", generator=g) * 2 - 1) * (4.0 / FAT_K ** 0.5)).half()
+    res = {}
+    for M, reps in ((16, 96), (2048, 16)):
+        a = torch.randn(M, FAT_K, dtype=torch.float16, device="cuda", generator=g)
+        out = torch.empty(M, FAT_N, dtype=torch.float32, device="cuda")
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+
+        def launch(c):
+            rc = L.exl3_fat_gemm(a.data_ptr(), trs[c % FAT_COPIES].data_ptr(), out.data_ptr(), svh.data_ptr(), M,
+                                 FAT_K, FAT_N, FAT_BITS, 2, stream.cuda_stream)
+            if rc:
+                raise RuntimeError(L.exl3_last_error().decode())
+
+        t = _graph_time(torch, stream, launch, reps)
+        nbytes = FAT_K * FAT_N * FAT_BITS // 8
+        flops = 2.0 * M * FAT_K * FAT_N
+        res[f"M{M}"] = {"us_per_call": round(t * 1e6, 2), "TFLOPs": round(flops / t / 1e12, 1),
+                        "pct_mfma_fp16_peak": round(100 * flops / t / 2.5e15, 2),
+                        "GBps_packed": round(nbytes / t / 1e9, 1), "pct_hbm_peak": round(100 * nbytes / t / 8e12, 2),
+                        "tokens_per_s": round(M / t, 1)}
+    return res
+
+
+def _graph_time(torch, stream, launch, reps):
+    with torch.cuda.stream(stream):
+        for c in range(3):
+            launch(c)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for c in range(reps):
+                launch(c)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+# ---------------------------------------------------------- large MoE (config 5)
+
+BIG_E, BIG_TOPK, BIG_H, BIG_I, BIG_M = 288, 8, 4096, 1536, 4
+BIG_ROUTINGS = 8  # rotating uniform routings: the experts touched change every call
+
+
+def big_moe_bench(torch):
+    """288 routed experts (uniform top-8) + 1 shared expert (always taken, weight
+    1) as one layer call, M=4 tokens; K in 2..5 with MCG (K=2, 4) and mul1
+    (K=3, 5)."""
+    res = {}
+    rng = np.random.default_rng(55)
+    E = BIG_E + 1  # the shared expert is expert BIG_E
+    routings = []
+    for r in range(BIG_ROUTINGS):
+        ids = np.stack([rng.choice(BIG_E, BIG_TOPK, replace=False) for _ in range(BIG_M)])
+        ids = np.concatenate([ids, np.full((BIG_M, 1), BIG_E)], axis=1).astype(np.int32)
+        w = rng.random((BIG_M, BIG_TOPK)).astype(np.float32)
+        w = np.concatenate([w / w.sum(1, keepdims=True), np.ones((BIG_M, 1), np.float32)], axis=1)
+        routings.append((torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), len(np.unique(ids))))
+    x = torch.randn(BIG_M, BIG_H, dtype=torch.float16, device="cuda")
+    for K, mcg in ((2, True), (3, False), (4, True), (5, False)):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(100 + K)
+        tabs = []
+        keep = []
+        for k, n in ((BIG_H, BIG_I), (BIG_H, BIG_I), (BIG_I, BIG_H)):
+            tr = torch.randint(-32768, 32768, (E, k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda",
+                               generator=g)
+            su = (torch.randint(0, 2, (E, k), device="cuda", generator=g) * 2 - 1).half()
+            sv = ((torch.randint(0, 2, (E, n), device="cuda", generator=g) * 2 - 1) * (4.0 / k ** 0.5)).half()
+            for a in (tr, su, sv):
+                keep.append(a)
+                tabs.append(torch.arange(E, dtype=torch.int64, device="cuda") * (a[0].numel() * a.element_size())
+                            + a.data_ptr())
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+
+        def launch(c):
+            ids, w, _ = routings[c % BIG_ROUTINGS]
+            torch.ops.sglang_exl3.exl3_moe_layer(x, ids, w, *tabs, K, K, K, mcg, BIG_I, 0.0)
+
+        t = _graph_time(torch, stream, launch, 48)
+        U = float(np.mean([u for _, _, u in routings]))
+        nbytes = U * 3 * BIG_H * BIG_I * K / 8
+        res[f"K{K}_{'mcg' if mcg else 'mul1'}"] = {
+            "us_per_layer": round(t * 1e6, 2), "tokens_per_s": round(BIG_M / t, 1), "unique_experts": round(U, 2),
+            "GBps": round(nbytes / t / 1e9, 1), "pct_hbm_peak": round(100 * nbytes / t / 8e12, 2)}
+        del keep, tabs
+        torch.cuda.empty_cache()
+    return res
+
+
 def profile_pass(torch, L, weights, steps):
     """Eager (non-graph) launches for rocprofv3: `steps` m=1 GEMVs over the rotating
     copies, then `steps` device copies of exactly one packed weight's bytes (the
@@ -279,6 +390,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the batched-MoE layer leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config-3 and config-5 legs")
     ap.add_argument("--profile-pass", action="store_true",
                     help="eager m=1 launches plus a copy-kernel calibration, for rocprofv3 counter runs")
     args = ap.parse_args()
@@ -289,9 +401,10 @@ def main():
 
     import torch
 
-    from sglang_exl3 import _lib
+    from sglang_exl3 import _lib, ops
 
     L = _lib.lib()
+    ops.register_custom_ops()
     weights = []
     for c in range(NCOPY):
         weights.append([torch.from_numpy(a).cuda() for a in make_weight(K_DIM, N_DIM, BITS, seed=c)])
@@ -342,6 +455,11 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "gemv_sweep": sweep,
     }
+    if not args.no_extra:
+        result["fat_gate_up"] = {"config": "config 3: exl3_fat_gemm k=4096 n=2x14336 K=3 mul1, 8 rotating copies",
+                                 **fat_bench(torch, L)}
+        result["large_moe"] = {"config": "config 5: 288 experts top-8 uniform + shared, h=4096 I=1536, M=4, "
+                                         "8 rotating routings", **big_moe_bench(torch)}
     if not args.no_moe:
         result["moe_layer"] = {"config": "config 4: E=128 top-8 hidden 2048 inter 768 K=3 MCG, "
                                          f"{MOE_LAYERS} rotating layer copies",
