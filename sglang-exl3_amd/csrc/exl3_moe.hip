@@ -224,61 +224,41 @@ double expected_active(int tokens, int topk, int E) {
     return u < cap ? u : cap;
 }
 
-// Launch shape of one expert projection pass.  Items = units x column blocks
-// x projections x k-splits; each item keeps 4 kw waves busy for ns steps.
-// From the most work per wave down, take the first shape with enough waves
-// for the device (`target`) whose split partials stay a small fraction of the
-// weight bytes; failing both, the best compromise.
+// Launch shape of one expert projection pass, by a rule fitted to graph-timed
+// sweeps on MI355X (config 4 at B = 1/16/64 and config 5):
+//  * few units (< 16): 2 k-waves x 4 steps per workgroup and more k-splits
+//    (latency-bound, parallelism matters);
+//  * otherwise 1 k-wave x 8 steps (4 where 32 k-slices do not divide k);
+//  * column blocks per item grouped only when the items would exceed about
+//    eight times the persistent grid (two 8-wave workgroups per CU).
+// Env overrides (tuning): EXL3_MOE_NSTEPS, EXL3_MOE_KW, EXL3_MOE_BPI.
 MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
-    const int kslices = k / 16;
-    // two 8-wave workgroups per CU when the LDS allows it (the kernel's
-    // register budget is set for that)
-    const size_t lds_two = kMaxLds / 2 - 1024;
-    const double target = env_int("EXL3_MOE_TARGET_WAVES", 3072);
-    const double max_traffic = env_int("EXL3_MOE_MAX_PARTIAL_PCT", 15) / 100.0;
-    const int f_steps = env_int("EXL3_MOE_NSTEPS", 0), f_kw = env_int("EXL3_MOE_KW", 0);
-    const double cols = (double)(n / 128) * nproj;
-    const double weight_bytes = units * cols * 128.0 * k * 4 / 8;  // nominal 4 bits
-    MoePlan best{0, 0, 0};
-    double best_score = -1;
-    for (int kw = 2; kw >= 1; --kw) {
-        for (int ns = 16; ns >= 2; ns /= 2) {
-            const int kts_wg = 4 * ns * kw;
-            if (kts_wg % 8 || kslices % kts_wg) continue;
-            if (moe_smem_bytes(kts_wg, kw) > lds_two) continue;
-            if ((f_steps && ns != f_steps) || (f_kw && kw != f_kw)) continue;
-            const int S = kslices / kts_wg;
-            const double waves = units * cols * S * 4 * kw;
-            const double traffic = S > 1 ? 2.0 * entries * 512.0 * cols * S / weight_bytes : 0.0;
-            // 1 when both goals hold; otherwise the worse of the two ratios
-            const double score = fmin(1.0, fmin(waves / target, traffic > 0 ? max_traffic / traffic : 1.0));
-            if (score > best_score + 1e-9) {
-                best = MoePlan{ns, kw, S, 1};
-                best_score = score;
-            }
+    (void)entries;
+    const int kslices = k / 16, nblk = n / 128;
+    const double grid = 512.0;
+    const bool few = units < 16.0;
+    int kw = env_int("EXL3_MOE_KW", few ? 2 : 1);
+    if (kw != 1 && kw != 2) kw = 1;
+    int ns = env_int("EXL3_MOE_NSTEPS", few ? 4 : 8);
+    while (ns > 2 && (kslices % (4 * ns * kw) || (4 * ns * kw) % 8 ||
+                      moe_smem_bytes(4 * ns * kw, kw) > kMaxLds / 2 - 1024))
+        ns /= 2;
+    if (kslices % (4 * ns * kw) || (4 * ns * kw) % 8) {  // k = 128 x odd: 2 steps of 1 wave always divide
+        ns = 2;
+        kw = 1;
+    }
+    const int S = kslices / (4 * ns * kw);
+    int bpi = env_int("EXL3_MOE_BPI", 0);
+    if (bpi <= 0 || nblk % bpi) {
+        bpi = 1;
+        while (units * (nblk / bpi) * nproj * S > 8.0 * grid) {
+            int nb = bpi + 1;
+            while (nb <= nblk && nblk % nb) ++nb;
+            if (nb > nblk) break;
+            bpi = nb;
         }
     }
-    if (best.ns == 0) best = MoePlan{2, 1, kslices / 8, 1};
-    // Column blocks per item: an item stages (and rotates) its rows once for
-    // all of its blocks.  With several rows per unit that staging is the
-    // larger cost, so group blocks as long as the items still fill the device
-    // twice over; with one row per unit keep one block per item (parallelism).
-    const double rows_per_unit = units > 0 ? fmin((double)MOE_UNIT_ROWS, entries / units) : 1.0;
-    const int nblk = n / 128;
-    const int f_bpi = env_int("EXL3_MOE_BPI", 0);
-    if (f_bpi > 0 && nblk % f_bpi == 0) {
-        best.bpi = f_bpi;
-    } else if (rows_per_unit >= 4.0) {
-        const double wg_target = 2.0 * 512;  // 2 workgroups x 256 CUs, twice over
-        for (int bpi = nblk; bpi >= 1; --bpi) {
-            if (nblk % bpi) continue;
-            if (units * (nblk / bpi) * nproj * best.splits >= wg_target || bpi == 1) {
-                best.bpi = bpi;
-                break;
-            }
-        }
-    }
-    return best;
+    return MoePlan{ns, kw, S, bpi};
 }
 
 struct MoeLayout {
