@@ -26,12 +26,19 @@ inline int launch_status(const char* what) {
     return EXL3_OK;
 }
 
-// Workspace layout shared by every split-k kernel: a fixed region of int
-// counters first (zero between calls; each call's last workgroups reset the
-// ones they used), then the fp32 partial sums.  The fixed offset keeps one
-// call's partials from ever overlapping another shape's counters.
+// Workspace layout shared by every kernel that needs one:
+//   [0, 256 KiB)          int counters of the split-k hand-offs;
+//   [256 KiB, 4.25 MiB)   64-bit fixed-point output accumulators of the
+//                         balanced GEMV;
+//   [4.25 MiB, ...)       per-call scratch (partials, staged rows, ...).
+// The first two regions are zero between calls (the caller zeroes the buffer
+// once; every kernel resets what it used).  Scratch starts at a fixed offset,
+// so no call's scratch ever overlaps the zeroed regions.
 constexpr size_t kWsCounterBytes = 256 * 1024;
 constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int);
+constexpr size_t kWsAccOffset = kWsCounterBytes;
+constexpr size_t kWsAccBytes = 4 * 1024 * 1024;
+constexpr size_t kWsScratchOffset = kWsAccOffset + kWsAccBytes;
 
 // LDS a gfx950 workgroup may allocate.
 constexpr size_t kMaxLds = 160 * 1024;

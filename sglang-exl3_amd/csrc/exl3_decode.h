@@ -139,6 +139,24 @@ __device__ __forceinline__ uint32_t window(const uint32_t* buf) {
     }
 }
 
+// Same window, with the straddling ones cut from the "middle words"
+// mid[j] = bits 16..47 of buf[j]:buf[j+1] (one v_alignbit per word boundary,
+// shared by every window crossing it) by a single v_bfe each.
+template <int K, int U>
+__device__ __forceinline__ uint32_t window_mid(const uint32_t* buf, const uint32_t* mid) {
+    constexpr int rel_end = 32 + (U + 1) * K;
+    constexpr int rel_start = rel_end - 16;
+    constexpr int ia = rel_start / 32;
+    constexpr int ib = (rel_end - 1) / 32;
+    constexpr int sh = 32 * (ib + 1) - rel_end;
+    if constexpr (ia == ib) {
+        return __builtin_amdgcn_ubfe(buf[ib], sh, 16);
+    } else {
+        static_assert(sh > 16 && sh < 32, "a straddling window starts inside the middle word");
+        return __builtin_amdgcn_ubfe(mid[ia], sh - 16, 16);
+    }
+}
+
 // ---------------------------------------------------------------- codebooks
 
 // x = state * M (+ 64248484 for 3INST) mod 2^32.  v_mul_lo_u32 issues at the

@@ -122,12 +122,12 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 
 }  // namespace
 
-// Prefill path of exl3_gemm (m > 64).  Scratch after the workspace's counter
-// region (shared with the GEMV kernels, which need it to stay zero):
-// [counters][xr fp16 m*k][out fp32 m*n].
+// Prefill path of exl3_gemm (m > 64).  Scratch after the workspace's zeroed
+// regions (shared with the GEMV kernels, which need them to stay zero):
+// [counters][accumulators][xr fp16 m*k][out fp32 m*n].
 size_t fat_xr_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
 size_t fat_gemm_scratch_bytes(int m, int k, int n) {
-    return kWsCounterBytes + fat_xr_bytes(m, k) + (size_t)m * n * 4;
+    return kWsScratchOffset + fat_xr_bytes(m, k) + (size_t)m * n * 4;
 }
 
 int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,
@@ -137,8 +137,8 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
                       "exl3_gemm: %zu workspace bytes needed for m=%d, %zu given", need, m,
                       ws ? ws_bytes : (size_t)0);
     EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4), "exl3_gemm: misaligned pointer");
-    __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsCounterBytes);
-    float* o32 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsCounterBytes + fat_xr_bytes(m, k));
+    __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsScratchOffset);
+    float* o32 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsScratchOffset + fat_xr_bytes(m, k));
     const long long chunks = (long long)m * (k / 128);
     rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x),
                                                                       reinterpret_cast<const __half*>(suh), xr, chunks,

@@ -4,7 +4,7 @@
 // csrc/quant/exl3_kernel_map.cuh:53-62).
 #include <stdlib.h>
 
-#include "exl3_gemv_impl.h"
+#include "exl3_gemv_sk.h"
 
 namespace exl3 {
 
@@ -16,6 +16,30 @@ int gemv_launch_K5(int, int, const GemvParams&, int, hipStream_t);
 int gemv_launch_K6(int, int, const GemvParams&, int, hipStream_t);
 int gemv_launch_K7(int, int, const GemvParams&, int, hipStream_t);
 int gemv_launch_K8(int, int, const GemvParams&, int, hipStream_t);
+
+int gemv_sk_launch_K1(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K2(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K3(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K4(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K5(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K6(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K7(int, int, const GemvSkParams&, hipStream_t);
+int gemv_sk_launch_K8(int, int, const GemvSkParams&, hipStream_t);
+
+int gemv_sk_launch(int K, int cb, int ns, const GemvSkParams& p, hipStream_t st) {
+    switch (K) {
+        case 1: return gemv_sk_launch_K1(cb, ns, p, st);
+        case 2: return gemv_sk_launch_K2(cb, ns, p, st);
+        case 3: return gemv_sk_launch_K3(cb, ns, p, st);
+        case 4: return gemv_sk_launch_K4(cb, ns, p, st);
+        case 5: return gemv_sk_launch_K5(cb, ns, p, st);
+        case 6: return gemv_sk_launch_K6(cb, ns, p, st);
+        case 7: return gemv_sk_launch_K7(cb, ns, p, st);
+        case 8: return gemv_sk_launch_K8(cb, ns, p, st);
+    }
+    set_error("exl3 gemv: K=%d outside 1..8", K);
+    return EXL3_ERR_UNSUPPORTED;
+}
 
 int gemv_launch(int K, int cb, int mb, const GemvParams& p, int experts, hipStream_t st) {
     switch (K) {
@@ -45,6 +69,7 @@ struct GemvPlan {
     int nsteps;  // steps of 4 k-slices per wave
     int kw;      // k waves per workgroup
     int splits;  // workgroups along k
+    int sk;      // 1: balanced kernel (gemv_sk_kernel): splits = pieces per column block, nsteps = longest piece
 };
 
 int env_int(const char* name, int dflt) {
@@ -59,15 +84,55 @@ int env_int(const char* name, int dflt) {
 // and take the first shape that puts at least `target` waves on the device
 // (1024 SIMDs: ~3 waves each hide HBM and MFMA latency); this also keeps the
 // number of cross-workgroup k-splits (the costly reduction) minimal.
+// Balanced kernel shape: P pieces per 128-column block, each of
+// ceil(k/64 / P) k-steps or one fewer (P with an instantiated step count).
+// Cost model fitted to graph-timed sweeps on MI355X (m = 1; k x n from
+// 2048 x 6144 to 14336 x 4096): with W = ceil(workgroups / CUs) workgroups on
+// the busiest CU and `steps` k-steps on it,
+//   time ~ 0.242 us * steps + 0.089 us * W + 0.902 us / min(W, 4)
+// (per-step work, per-workgroup overhead, and the latency that fewer than
+// four workgroups per CU leave exposed).  Used for m = 1; from m = 2 on the
+// per-workgroup input rotation grows with m and the k-split kernel is faster
+// (measured at m = 2, 4, 8).
+// Returns false when the balanced kernel does not apply.
+bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {
+    if (experts != 1 || m > env_int("EXL3_GEMV_SK_MAX_M", 1) || env_int("EXL3_GEMV_SK", 1) == 0) return false;
+    if ((size_t)m * n * 8 > kWsAccBytes) return false;
+    const int ks_blk = k / 64;
+    const long long nblk = n / 128;
+    const int forced = env_int("EXL3_GEMV_SK_P", 0);
+    const long long cus = 256;
+    double best_cost = 1e30;
+    bool found = false;
+    for (int P = 1; P <= ks_blk && P <= SK_MAX_CONTRIB; ++P) {
+        if (forced && P != forced) continue;
+        const int ns = (ks_blk + P - 1) / P;  // pieces of ns - 1 or ns k-steps
+        bool inst = false;
+        for (int c : kSkSteps) inst |= c == ns;
+        if (!inst || gemv_sk_smem_bytes(m, ns) > kMaxGemvSmem) continue;
+        const long long W = (nblk * P + cus - 1) / cus;
+        const double cost = 0.242 * (double)(W * ns) + 0.089 * (double)W + 0.902 / (double)(W < 4 ? W : 4);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            *ns_out = ns;
+            *p_out = P;
+            found = true;
+        }
+    }
+    return found;
+}
+
 GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
     GemvPlan pl;
+    int sk_ns = 0, sk_p = 0;
+    if (plan_gemv_sk(m, k, n, experts, &sk_ns, &sk_p)) return GemvPlan{1, sk_ns, 1, sk_p, 1};
     pl.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     const int kslices = k / 16;
     const int max_steps = 16;
     const long long target = env_int("EXL3_GEMV_TARGET_WAVES", 3072);
     const int f_steps = env_int("EXL3_GEMV_NSTEPS", 0), f_kw = env_int("EXL3_GEMV_KW", 0);
     const long long cols = (long long)(n / 128) * experts;
-    GemvPlan best{pl.mb, 0, 0, 0};
+    GemvPlan best{pl.mb, 0, 0, 0, 0};
     long long best_waves = -1;
     for (int kw = 2; kw >= 1; --kw) {
         for (int ns = max_steps; ns >= 2; ns /= 2) {  // instantiated step counts: 16, 8, 4, 2
@@ -79,23 +144,24 @@ GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
             const long long waves = cols * S * 4 * kw;
             if (waves >= target) {
                 if (best_waves < target || S < best.splits) {
-                    best = GemvPlan{pl.mb, ns, kw, S};
+                    best = GemvPlan{pl.mb, ns, kw, S, 0};
                     best_waves = waves;
                 }
             } else if (best_waves < target && waves > best_waves) {
-                best = GemvPlan{pl.mb, ns, kw, S};
+                best = GemvPlan{pl.mb, ns, kw, S, 0};
                 best_waves = waves;
             }
         }
     }
-    if (best.nsteps == 0) best = GemvPlan{pl.mb, 2, 1, kslices / 8};  // 128-row ranges always fit
+    if (best.nsteps == 0) best = GemvPlan{pl.mb, 2, 1, kslices / 8, 0};  // 128-row ranges always fit
     return best;
 }
 
 size_t workspace_bytes_for(const GemvPlan& pl, int m, int n, int experts) {
+    if (pl.sk) return kWsAccOffset + (size_t)m * n * 8;
     if (pl.splits <= 1) return 0;
     const size_t nblk = (size_t)(n / 128) * experts;
-    return kWsCounterBytes + nblk * pl.splits * (size_t)m * 128 * sizeof(float);
+    return kWsScratchOffset + nblk * pl.splits * (size_t)m * 128 * sizeof(float);
 }
 
 int check_common(const char* fn, int m, int k, int n, int K, int codebook) {
@@ -113,6 +179,22 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
     const size_t need = workspace_bytes_for(pl, p.m, p.n, experts);
     EXL3_REQUIRE_CODE(need == 0 || (ws && ws_bytes >= need), EXL3_ERR_WORKSPACE,
                       "%s: workspace of %zu bytes needed, %zu given", fn, need, ws ? ws_bytes : (size_t)0);
+    if (pl.sk) {
+        GemvSkParams q{};
+        q.x = p.x;
+        q.trellis = p.trellis;
+        q.suh = p.suh;
+        q.svh = p.svh;
+        q.y = p.y;
+        q.acc = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + kWsAccOffset);
+        q.m = p.m;
+        q.k = p.k;
+        q.n = p.n;
+        q.ks_blk = p.k / 64;
+        q.pieces = pl.splits;
+        q.nwg = (p.n / 128) * pl.splits;
+        return gemv_sk_launch(K, codebook, pl.nsteps, q, st);
+    }
     p.nsteps = pl.nsteps;
     p.kw = pl.kw;
     p.splits = pl.splits;
@@ -121,7 +203,7 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
                           "%s: %d column blocks exceed the %zu workspace counters", fn, (p.n / 128) * experts,
                           kWsMaxCounters);
         p.counters = reinterpret_cast<int*>(ws);
-        p.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsCounterBytes);
+        p.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsScratchOffset);
     } else {
         p.counters = nullptr;
         p.partials = nullptr;
@@ -166,7 +248,7 @@ extern "C" int exl3_gemv_plan(int m, int k, int n, int K, int experts, int* out)
     out[1] = pl.nsteps;
     out[2] = pl.kw;
     out[3] = pl.splits;
-    out[4] = (int)gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw);
+    out[4] = (int)(pl.sk ? gemv_sk_smem_bytes(mc, pl.nsteps) : gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw));
     return EXL3_OK;
 }
 

@@ -279,7 +279,7 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     const double units = act * ceil(per / MOE_UNIT_ROWS);
     L.gu = plan_moe(units, L.entries, hidden, inter, 2);
     L.dn = plan_moe(units, L.entries, inter, hidden, 1);
-    size_t o = kWsCounterBytes;
+    size_t o = kWsScratchOffset;
     L.route_off = o;
     o = align256(o + 2 * sizeof(int));
     L.units_off = o;

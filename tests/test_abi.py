@@ -64,26 +64,45 @@ def test_batched_rejects_bad_arguments():
     assert b"num_active" in L.exl3_last_error()
 
 
+SK_STEPS = (1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16)
+
+
+def _check_plan(m, k, n, K, experts=1):
+    out = (ctypes.c_int * 5)()
+    assert _lib.lib().exl3_gemv_plan(m, k, n, K, experts, out) == 0
+    mb, ns, kw, splits, lds = list(out)
+    assert 16 * mb >= m and 0 < lds <= 160 * 1024
+    balanced = experts == 1 and m <= 1 and m * n * 8 <= 4 * 1024 * 1024 and os.environ.get("EXL3_GEMV_SK") != "0"
+    if balanced:
+        # balanced kernel: each column block's k/64 k-steps in `splits` pieces of at most ns steps
+        ks_blk = k // 64
+        assert kw == 1 and 1 <= splits <= min(63, ks_blk)
+        assert ns == -(-ks_blk // splits) and ns in SK_STEPS
+    else:
+        # k-split kernel: k-slices covered exactly once, whole 128-row rotation blocks per workgroup
+        assert 4 * ns * kw * splits == k // 16
+        assert (4 * ns * kw) % 8 == 0
+    return out
+
+
 def test_workspace_and_plan_are_host_only():
     L = _lib.lib()
-    assert L.exl3_gemv_workspace_size(1, 4096, 14336, 4, 1) > 0
-    out = (ctypes.c_int * 5)()
-    assert L.exl3_gemv_plan(1, 4096, 14336, 4, 1, out) == 0
-    mb, ns, kw, splits, lds = list(out)
-    assert mb == 1 and ns in (2, 4, 8, 16) and kw in (1, 2)
-    assert 4 * ns * kw * splits == 4096 // 16  # k-slices covered exactly once
-    assert 0 < lds <= 160 * 1024
+    # the balanced kernel needs the counter region plus one 8-byte accumulator per output
+    assert L.exl3_gemv_workspace_size(1, 4096, 14336, 4, 1) >= 256 * 1024 + 14336 * 8
+    _check_plan(1, 4096, 14336, 4)
 
 
 @pytest.mark.parametrize("m,k,n,K", [(1, 128, 128, 1), (8, 768, 2048, 3), (16, 2048, 768, 3), (64, 256, 256, 2),
-                                     (4, 4096, 1536, 5), (2, 14336, 4096, 4)])
-def test_plan_covers_k_exactly(m, k, n, K):
-    out = (ctypes.c_int * 5)()
-    assert _lib.lib().exl3_gemv_plan(m, k, n, K, 1, out) == 0
-    mb, ns, kw, splits, lds = list(out)
-    assert 16 * mb >= m
-    assert 4 * ns * kw * splits == k // 16
-    assert (4 * ns * kw) % 8 == 0  # whole 128-row rotation blocks per workgroup
+                                     (4, 4096, 1536, 5), (2, 14336, 4096, 4), (17, 1024, 512, 4)])
+def test_plan_covers_k(m, k, n, K):
+    _check_plan(m, k, n, K)
+    _check_plan(m, k, n, K, experts=3)  # batched form: k-split kernel
+
+
+def test_split_plan_when_balanced_disabled(monkeypatch):
+    monkeypatch.setenv("EXL3_GEMV_SK", "0")
+    out = _check_plan(1, 4096, 14336, 4)
+    assert 4 * out[1] * out[2] * out[3] == 4096 // 16
 
 
 def test_codebook_flag_mapping_matches_reference():

@@ -156,3 +156,85 @@ def test_gemv_rejects_bad_shapes():
         torch.ops.sglang_exl3.exl3_gemv(xd[:, :128].contiguous(), tr, su, sv, 4, True, 1)
     with pytest.raises(RuntimeError):
         torch.ops.sglang_exl3.exl3_gemv(xd.cpu(), tr, su, sv, 4, True, 1)
+
+
+def _with_env(env, fn):
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return fn()
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("m,k,n,K,cb,pieces", [
+    # k=512: 8 k-steps per column block cut into 3, 5 or 7 uneven pieces; every codebook
+    (1, 512, 384, 4, 1, 3), (1, 512, 384, 4, 1, 5), (2, 512, 384, 3, 2, 7), (5, 512, 384, 2, 0, 5),
+    (16, 512, 384, 4, 1, 1), (3, 768, 256, 5, 2, 2), (1, 256, 512, 3, 1, 4), (8, 1024, 256, 6, 1, 3),
+    (1, 2048, 128, 4, 1, 9), (4, 640, 640, 4, 2, 4), (1, 256, 256, 8, 0, 3), (1, 4096, 256, 4, 1, 63),
+])
+def test_gemv_balanced_pieces(m, k, n, K, cb, pieces):
+    """Balanced kernel at forced piece counts: uneven pieces of each column block's k range,
+    up to the 63-contribution limit of the fixed-point accumulators, every codebook."""
+    print(f"case: balanced gemv m={m} k={k} n={n} K={K} cb={cb} pieces={pieces}", flush=True)
+    trellis, suh, svh = make_weight(k, n, K, seed=700 + pieces + 3 * K + cb)
+    x = make_x(m, k, seed=701 + m + pieces)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    ks_blk = k // 64
+    ns = -(-ks_blk // pieces)
+    env = {"EXL3_GEMV_SK_P": pieces, "EXL3_GEMV_SK_MAX_M": 16}  # the kernel serves m <= 16; the planner picks it for m = 1
+    plan = _with_env(env, lambda: _plan(m, k, n, K))
+    assert plan[1] == ns and plan[2] == 1 and plan[3] == pieces
+    ys = [_with_env(env, lambda: _run_capi(xd, tr, su, sv, K, cb)) for _ in range(2)]
+    torch.cuda.synchronize()
+    ref = _oracle_ref(x, trellis, suh, svh, K, cb)
+    check_close(ys[0].float().cpu().numpy(), ref, f"balanced m={m} pieces={pieces}")
+    # a second call on the same workspace gives the same bits (accumulators were cleared)
+    assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
+
+
+def _plan(m, k, n, K):
+    import ctypes
+    out = (ctypes.c_int * 5)()
+    _lib.check(_lib.lib().exl3_gemv_plan(m, k, n, K, 1, out), "exl3_gemv_plan")
+    return list(out)
+
+
+@pytest.mark.parametrize("m,k,n,K,cb", [(1, 512, 256, 4, 1), (8, 256, 384, 3, 2), (16, 512, 256, 2, 0)])
+def test_gemv_split_kernel_vs_oracle(m, k, n, K, cb):
+    """The k-split kernel (batched form, m > 16) on single-matrix problems too."""
+    print(f"case: split gemv m={m} k={k} n={n} K={K} cb={cb}", flush=True)
+    trellis, suh, svh = make_weight(k, n, K, seed=800 + m + K)
+    x = make_x(m, k, seed=801 + m)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    assert _with_env({"EXL3_GEMV_SK": 0}, lambda: _plan(m, k, n, K))[2] >= 1
+    y = _with_env({"EXL3_GEMV_SK": 0}, lambda: _run_capi(xd, tr, su, sv, K, cb))
+    ref = _oracle_ref(x, trellis, suh, svh, K, cb)
+    check_close(y.float().cpu().numpy(), ref, f"split m={m}")
+
+
+def test_gemv_balanced_leaves_accumulators_zero():
+    """Every output element's fixed-point accumulator is cleared by the workgroup that
+    completes it, so the workspace's zero regions are zero after each call."""
+    m, k, n, K = 1, 1024, 2048, 4
+    assert _plan(m, k, n, K)[2] == 1  # the balanced kernel serves m = 1
+    trellis, suh, svh = make_weight(k, n, K, seed=900)
+    x = make_x(m, k, seed=901)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    L = _lib.lib()
+    need = int(L.exl3_gemv_workspace_size(m, k, n, K, 1))
+    assert need >= 256 * 1024 + m * n * 8
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    for _ in range(3):
+        _lib.check(L.exl3_gemv(xd.data_ptr(), tr.data_ptr(), su.data_ptr(), sv.data_ptr(), y.data_ptr(), m, k, n, K,
+                               1, ws.data_ptr(), ws.numel(), int(torch.cuda.current_stream().cuda_stream)),
+                   "exl3_gemv")
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(ws)) == 0
+    check_close(y.float().cpu().numpy(), _oracle_ref(x, trellis, suh, svh, K, 1), "balanced ws")
