@@ -69,7 +69,7 @@ struct GemvPlan {
     int nsteps;  // steps of 4 k-slices per wave
     int kw;      // k waves per workgroup
     int splits;  // workgroups along k
-    int sk;      // 1: balanced kernel (gemv_sk_kernel): splits = pieces per column block, nsteps = longest piece
+    int sk;      // 1: balanced kernel (gemv_sk_kernel, m = 1): splits = pieces per column block, nsteps = piece length
 };
 
 int env_int(const char* name, int dflt) {
@@ -84,20 +84,20 @@ int env_int(const char* name, int dflt) {
 // and take the first shape that puts at least `target` waves on the device
 // (1024 SIMDs: ~3 waves each hide HBM and MFMA latency); this also keeps the
 // number of cross-workgroup k-splits (the costly reduction) minimal.
-// Balanced kernel shape: P pieces per 128-column block, each of
-// ceil(k/64 / P) k-steps or one fewer (P with an instantiated step count).
-// Cost model fitted to graph-timed sweeps on MI355X (m = 1; k x n from
-// 2048 x 6144 to 14336 x 4096): with W = ceil(workgroups / CUs) workgroups on
-// the busiest CU and `steps` k-steps on it,
+// Balanced kernel shape (m = 1): P equal pieces per 128-column block, P a
+// divisor of k/64 with an instantiated piece length.  Cost model fitted to
+// graph-timed sweeps on MI355X (k x n from 2048 x 6144 to 14336 x 4096):
+// with W = ceil(workgroups / CUs) workgroups on the busiest CU and `steps`
+// k-steps on it,
 //   time ~ 0.242 us * steps + 0.089 us * W + 0.902 us / min(W, 4)
 // (per-step work, per-workgroup overhead, and the latency that fewer than
-// four workgroups per CU leave exposed).  Used for m = 1; from m = 2 on the
-// per-workgroup input rotation grows with m and the k-split kernel is faster
-// (measured at m = 2, 4, 8).
-// Returns false when the balanced kernel does not apply.
+// four workgroups per CU leave exposed).  From m = 2 on the k-split kernel is
+// used: the balanced kernel's per-workgroup input rotation grows with m
+// (measured at m = 2, 4, 8).  Returns false when the balanced kernel does not
+// apply.
 bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {
-    if (experts != 1 || m > env_int("EXL3_GEMV_SK_MAX_M", 1) || env_int("EXL3_GEMV_SK", 1) == 0) return false;
-    if ((size_t)m * n * 8 > kWsAccBytes) return false;
+    if (experts != 1 || m != 1 || env_int("EXL3_GEMV_SK", 1) == 0) return false;
+    if ((size_t)n * 8 > kWsAccBytes) return false;
     const int ks_blk = k / 64;
     const long long nblk = n / 128;
     const int forced = env_int("EXL3_GEMV_SK_P", 0);
@@ -105,11 +105,11 @@ bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {
     double best_cost = 1e30;
     bool found = false;
     for (int P = 1; P <= ks_blk && P <= SK_MAX_CONTRIB; ++P) {
-        if (forced && P != forced) continue;
-        const int ns = (ks_blk + P - 1) / P;  // pieces of ns - 1 or ns k-steps
+        if (ks_blk % P || (forced && P != forced)) continue;
+        const int ns = ks_blk / P;
         bool inst = false;
         for (int c : kSkSteps) inst |= c == ns;
-        if (!inst || gemv_sk_smem_bytes(m, ns) > kMaxGemvSmem) continue;
+        if (!inst || gemv_sk_smem_bytes(ns) > kMaxGemvSmem) continue;
         const long long W = (nblk * P + cus - 1) / cus;
         const double cost = 0.242 * (double)(W * ns) + 0.089 * (double)W + 0.902 / (double)(W < 4 ? W : 4);
         if (cost < best_cost - 1e-9) {
@@ -158,7 +158,7 @@ GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
 }
 
 size_t workspace_bytes_for(const GemvPlan& pl, int m, int n, int experts) {
-    if (pl.sk) return kWsAccOffset + (size_t)m * n * 8;
+    if (pl.sk) return kWsAccOffset + (size_t)n * 8;
     if (pl.splits <= 1) return 0;
     const size_t nblk = (size_t)(n / 128) * experts;
     return kWsScratchOffset + nblk * pl.splits * (size_t)m * 128 * sizeof(float);
@@ -187,12 +187,9 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
         q.svh = p.svh;
         q.y = p.y;
         q.acc = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + kWsAccOffset);
-        q.m = p.m;
         q.k = p.k;
         q.n = p.n;
-        q.ks_blk = p.k / 64;
         q.pieces = pl.splits;
-        q.nwg = (p.n / 128) * pl.splits;
         return gemv_sk_launch(K, codebook, pl.nsteps, q, st);
     }
     p.nsteps = pl.nsteps;
@@ -248,7 +245,7 @@ extern "C" int exl3_gemv_plan(int m, int k, int n, int K, int experts, int* out)
     out[1] = pl.nsteps;
     out[2] = pl.kw;
     out[3] = pl.splits;
-    out[4] = (int)(pl.sk ? gemv_sk_smem_bytes(mc, pl.nsteps) : gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw));
+    out[4] = (int)(pl.sk ? gemv_sk_smem_bytes(pl.nsteps) : gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw));
     return EXL3_OK;
 }
 

@@ -1,18 +1,18 @@
-// Balanced small-m EXL3 GEMV for gfx950: y = svh (.) H(x' . T) / sqrt(128).
+// Balanced single-row (bs = 1) EXL3 GEMV for gfx950: y = svh (.) H(x' . T) / sqrt(128).
 //
 // Same product as gemv_kernel (reference: csrc/quant/exl3_gemv_kernel.cuh:138-402),
 // organised for an even load on every SIMD and a one-round-trip k reduction:
 //
 //   * Each 128-column block's k range (k/64 "k-steps" of 64) is cut into P
-//     pieces whose sizes differ by at most one step; workgroup w (4 waves, one
-//     per 32 columns) computes piece w % P of block w / P.  The planner picks
-//     P so that the blocks x P workgroups spread evenly over the CUs.
+//     equal pieces; workgroup (pi, cb) (4 waves, one per 32 columns)
+//     computes piece pi of block cb.  The planner picks P so that the
+//     blocks x P workgroups spread evenly over the CUs.
 //   * Each workgroup rotates only the activation blocks its piece needs
 //     (x * suh, FWHT, / sqrt(128), fp16) into LDS in MFMA A-fragment order.
 //   * The decode/MFMA loop is gemv_kernel's (pair-form words, activations
 //     duplicated), with four independent accumulator chains.
-//   * Epilogue: the four waves' column slices meet in LDS, one wave per row
-//     applies the output FWHT, 1/sqrt(128) and svh, and adds the result into
+//   * Epilogue: the four waves' column slices meet in LDS, one wave applies
+//     the output FWHT, 1/sqrt(128) and svh, and adds the result into
 //     a 64-bit fixed-point accumulator per output element (atomic add with
 //     return).  The accumulator's top bits count the contributions; the
 //     workgroup whose add brings the count to P converts the sum to fp16,
@@ -50,26 +50,25 @@ __device__ __forceinline__ float sk_decode(unsigned long long total, int cnt) {
 }
 
 struct GemvSkParams {
-    const __half* x;          // [m][k]
+    const __half* x;          // [k] (one row)
     const uint32_t* trellis;  // [k/16][n/16][8K] words
     const __half* suh;        // [k]
     const __half* svh;        // [n]
-    __half* y;                // [m][n]
-    unsigned long long* acc;  // [m][n] fixed-point accumulators, zero between calls
-    int m, k, n;
-    int ks_blk;  // k-steps per column block (k / 64)
-    int pieces;  // P: workgroups per column block
-    int nwg;     // workgroups launched: (n / 128) * P
+    __half* y;                // [n]
+    unsigned long long* acc;  // [n] fixed-point accumulators, zero between calls
+    int k, n;
+    int pieces;  // P: workgroups per column block (grid.x); grid.y = n / 128
 };
 
-inline size_t gemv_sk_smem_bytes(int m, int ns) {
-    const size_t xs = ((size_t)ns * 4 * 4 * 8 * m * 2 + 16 + 15) & ~(size_t)15;  // A staging + zero fragment
-    const size_t xsum = ((size_t)m * ns * 4 + 15) & ~(size_t)15;                  // mul1: sum of x' per step
-    return xs + xsum + (size_t)m * 128 * 4;                                        // column tile
+inline size_t gemv_sk_smem_bytes(int ns) {
+    // A staging [NS * 4 k-tiles][4 quarters][8 halves] + zero fragment, x' sums
+    // per step (mul1), one 128-column fp32 tile
+    return (((size_t)ns * 128 * 2 + 16 + 15) & ~(size_t)15) + (((size_t)ns * 4 + 15) & ~(size_t)15) + 128 * 4;
 }
 
 // One MFMA B fragment (values u = 4F..4F+3 of the lane's group, pair form)
-// multiplied into its accumulator chain right after it is decoded.
+// multiplied into its accumulator chain (quarter parity x column tile) right
+// after it is decoded; the middle words mid[] serve the straddling windows.
 template <int K, int CB, int F>
 __device__ __forceinline__ void sk_frag(const uint32_t* buf, const uint32_t* mid, const half8_t (&A)[4],
                                         float4_t (&acc)[2][2]) {
@@ -92,28 +91,26 @@ __device__ __forceinline__ void sk_frags(const uint32_t* buf, const uint32_t* mi
 template <int K, int CB, int NS>
 __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
     constexpr int D = gv_depth<K>();
+    constexpr int kts = 4 * NS;  // k-slices staged
     extern __shared__ __align__(16) unsigned char sk_smem[];
 
-    const int m = p.m, k = p.k, n = p.n, ks_blk = p.ks_blk, P = p.pieces;
-    const int cb = blockIdx.x / P, pi = blockIdx.x - cb * P;
-    const int ks0 = (pi * ks_blk) / P;
-    const int nreal = ((pi + 1) * ks_blk) / P - ks0;  // NS - 1 or NS k-steps (NS = ceil(ks_blk / P))
+    const int n = p.n, P = p.pieces;
+    const int pi = blockIdx.x, cb = blockIdx.y;
+    const int ks0 = pi * NS;  // first k-step of the piece
 
     const int tid = threadIdx.x, cw = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
     const int ntiles = n >> 4;
-    constexpr int kts = 4 * NS;  // k-slices staged
 
     _Float16* xs = reinterpret_cast<_Float16*>(sk_smem);
-    const int xs_halves = kts * 4 * m * 8;
-    float* xsum = reinterpret_cast<float*>(sk_smem + (((size_t)xs_halves * 2 + 16 + 15) & ~(size_t)15));
-    float* ybuf = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(xsum) + (((size_t)m * NS * 4 + 15) & ~(size_t)15));
+    float* xsum = reinterpret_cast<float*>(sk_smem + (((size_t)NS * 128 * 2 + 16 + 15) & ~(size_t)15));
+    float* ybuf = xsum + ((NS + 3) & ~3);
 
-    // rotation work: the 128-blocks j0..j0+nblocks-1 holding the piece's k-steps, every row
+    // rotation work: the 128-blocks j0..j0+nblocks-1 holding the piece's k-steps
     const int j0 = ks0 >> 1;
-    const int nblocks = ((ks0 + nreal - 1) >> 1) - j0 + 1;
+    const int nblocks = ((ks0 + NS - 1) >> 1) - j0 + 1;
 
-    // 1. activations of this wave's first block (row 0), then the weights
+    // 1. activations of this wave's first block, then the weights
     const EXL3_GLOBAL __half* xg = gptr(p.x) + 2 * lane;
     const EXL3_GLOBAL __half* suhg = gptr(p.suh) + 2 * lane;
     __half2 x0 = __float2half2_rn(0.f), s0 = x0;
@@ -127,62 +124,61 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
     const __half2 svv = ld_h2(gptr(p.svh) + cb * 128 + 2 * lane);
     uint32_t w[D][K];
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < nreal ? d : nreal - 1) * ss, w[d]);
+    for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < NS ? d : NS - 1) * ss, w[d]);
 
     // 2. input rotation into LDS (A order, each value duplicated).  A lane
     //    holds k = 128 j + 2 lane (+1): k-step 2j + lane/32, offset (2 lane) % 64
     //    inside it, so its LDS slot is a per-lane constant plus 128 halves per
-    //    local step and 32 kts halves per row.
-    if (tid < 8) xs[xs_halves + tid] = (_Float16)0.0f;
+    //    local step.
+    if (tid < 8) xs[NS * 128 + tid] = (_Float16)0.0f;
     const int xs_lane = xs_index((2 * lane) & 63, 0, kts);
     for (int jb = cw; jb < nblocks; jb += 4) {
         const int j = j0 + jb;
         const int l = 2 * j + (lane >> 5) - ks0;  // local step of this lane's values
-        const bool mine = l >= 0 && l < nreal;
+        const bool mine = l >= 0 && l < NS;
+        const __half2 xv = jb == cw ? x0 : ld_h2(xg + j * 128);
         const __half2 sv = jb == cw ? s0 : ld_h2(suhg + j * 128);
-        for (int row = 0; row < m; ++row) {
-            const __half2 xv = (jb == cw && row == 0) ? x0 : ld_h2(xg + (size_t)row * k + j * 128);
-            const __half2 pr = __hmul2(xv, sv);
-            float a = __low2float(pr), c = __high2float(pr);
-            fwht128_pair_f(a, c, lane);
-            const _Float16 ha = (_Float16)(a * kHadNorm), hc = (_Float16)(c * kHadNorm);
-            if (mine) {
-                const int ia = xs_lane + row * kts * 32 + l * 128;
-                xs[ia] = ha;
-                xs[ia + 1] = ha;
-                xs[ia + 2] = hc;
-                xs[ia + 3] = hc;
-            }
-            if constexpr (CB == 2) {
-                // per-step sums over each half of the wave (lanes 0-31: k-step 2j, 32-63: 2j+1)
-                float t = mine ? (float)ha + (float)hc : 0.f;
-                t += lane_xor<16>(t);
-                t += lane_xor<8>(t);
-                t += lane_xor<4>(t);
-                t += lane_xor<2>(t);
-                t += lane_xor<1>(t);
-                if ((lane & 31) == 0 && mine) xsum[row * NS + l] = t;
-            }
+        const __half2 pr = __hmul2(xv, sv);
+        float a = __low2float(pr), c = __high2float(pr);
+        fwht128_pair_f(a, c, lane);
+        const _Float16 ha = (_Float16)(a * kHadNorm), hc = (_Float16)(c * kHadNorm);
+        if (mine) {
+            const int ia = xs_lane + l * 128;
+            xs[ia] = ha;
+            xs[ia + 1] = ha;
+            xs[ia + 2] = hc;
+            xs[ia + 3] = hc;
+        }
+        if constexpr (CB == 2) {
+            // per-step sums over each half of the wave (lanes 0-31: k-step 2j, 32-63: 2j+1)
+            float t = mine ? (float)ha + (float)hc : 0.f;
+            t += lane_xor<16>(t);
+            t += lane_xor<8>(t);
+            t += lane_xor<4>(t);
+            t += lane_xor<2>(t);
+            t += lane_xor<1>(t);
+            if ((lane & 31) == 0 && mine) xsum[l] = t;
         }
     }
     __syncthreads();
 
-    // 3. decode + MFMA; four accumulator chains (quarter parity x column tile)
+    // 3. decode + MFMA; four accumulator chains (quarter parity x column tile).
+    //    The one activation row is A row 0: lanes with i = 0 read it, the
+    //    others keep zero fragments.
     float4_t acc[2][2];
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
         acc[a][0] = float4_t{0.f, 0.f, 0.f, 0.f};
         acc[a][1] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
-    const bool a_live = i < m;
-    const _Float16* a_base = xs + (size_t)((a_live ? i : 0) * kts + g) * 4 * 8;
+    const bool a_live = i == 0;
+    const _Float16* a_base = xs + g * 32;
     const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;  // lane of group q - 1 (mod 8)
     half8_t A[4];
 #pragma unroll
     for (int Q = 0; Q < 4; ++Q) A[Q] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        if (s == NS - 1 && nreal < NS) break;  // the shorter pieces skip the last step (uniform)
         const int d = s % D;
         uint32_t buf[K + 1];
 #pragma unroll
@@ -200,72 +196,64 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
         // decode fragment by fragment, each MFMA issued as soon as its
         // fragment is ready so the matrix core runs under the next decode
         sk_frags<K, CB>(buf, mid, A, acc, std::make_integer_sequence<int, 8>{});
-        // prefetch; the shorter pieces re-read their last step instead of branching
-        if (s + D < NS) load_words<K>(tb + (size_t)(s + D < nreal ? s + D : nreal - 1) * ss, w[d]);
-#ifndef EXL3_SK_NO_INTERLEAVE
+        if (s + D < NS) load_words<K>(tb + (size_t)(s + D) * ss, w[d]);
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
             __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         }
-#endif
     }
-    // column tile: lane (g, i) holds rows 4g + r, column cw*32 + (i >> 3)*16 + (i & 7) + 8c
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 4 * g + r;
-            const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-            if (row < m) ybuf[row * 128 + col] = acc[0][c][r] + acc[1][c][r];
-        }
+    // output row 0 sits in lanes with g = 0 (element r = 0): column
+    // cw*32 + (i >> 3)*16 + (i & 7) + 8c
+    if (g == 0) {
+        const int col = cw * 32 + (i >> 3) * 16 + (i & 7);
+        ybuf[col] = acc[0][0][0] + acc[1][0][0];
+        ybuf[col + 8] = acc[0][1][0] + acc[1][1][0];
+    }
     __syncthreads();
+    if (cw != 0) return;
 
-    // 4. output FWHT, scale, fixed-point accumulate; the completing workgroup
-    //    writes fp16 and clears
+    // 4. output FWHT, scale, fixed-point accumulate; the workgroup completing
+    //    an element writes fp16 and clears its accumulator
+    float a = ybuf[2 * lane], b = ybuf[2 * lane + 1];
+    if constexpr (CB == 2) {
+        float sx = 0.f;
+#pragma unroll
+        for (int l = 0; l < NS; ++l) sx += xsum[l];
+        a = a * kMul1Kinv + kMul1Delta * sx;
+        b = b * kMul1Kinv + kMul1Delta * sx;
+    }
+    fwht128_pair_f(a, b, lane);
+    a = a * kHadNorm * __low2float(svv);
+    b = b * kHadNorm * __high2float(svv);
+    const int e0 = cb * 128 + 2 * lane;
+    unsigned long long* acc0 = p.acc + e0;
+    const unsigned long long ea = sk_encode(a), eb = sk_encode(b);
+    const unsigned long long oa = __hip_atomic_fetch_add(acc0, ea, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long ob = __hip_atomic_fetch_add(acc0 + 1, eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     EXL3_GLOBAL __half* y = gptr(p.y);
-    const float sva = __low2float(svv), svb = __high2float(svv);
-    for (int row = cw; row < m; row += 4) {
-        float a = ybuf[row * 128 + 2 * lane], b = ybuf[row * 128 + 2 * lane + 1];
-        if constexpr (CB == 2) {
-            float sx = 0.f;
-            for (int l = 0; l < nreal; ++l) sx += xsum[row * NS + l];
-            a = a * kMul1Kinv + kMul1Delta * sx;
-            b = b * kMul1Kinv + kMul1Delta * sx;
-        }
-        fwht128_pair_f(a, b, lane);
-        a = a * kHadNorm * sva;
-        b = b * kHadNorm * svb;
-        const size_t e0 = (size_t)row * n + cb * 128 + 2 * lane;
-        unsigned long long* acc0 = p.acc + e0;
-        const unsigned long long ea = sk_encode(a), eb = sk_encode(b);
-        const unsigned long long oa = __hip_atomic_fetch_add(acc0, ea, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long ob = __hip_atomic_fetch_add(acc0 + 1, eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((int)(oa >> SK_CNT_SHIFT) == P - 1) {
-            const __half h = __float2half_rn(sk_decode(oa + ea, P));
-            *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + e0) = __half_as_ushort(h);
-            __hip_atomic_store(acc0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if ((int)(ob >> SK_CNT_SHIFT) == P - 1) {
-            const __half h = __float2half_rn(sk_decode(ob + eb, P));
-            *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + e0 + 1) = __half_as_ushort(h);
-            __hip_atomic_store(acc0 + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    if ((int)(oa >> SK_CNT_SHIFT) == P - 1) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + e0) = __half_as_ushort(__float2half_rn(sk_decode(oa + ea, P)));
+        __hip_atomic_store(acc0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if ((int)(ob >> SK_CNT_SHIFT) == P - 1) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + e0 + 1) = __half_as_ushort(__float2half_rn(sk_decode(ob + eb, P)));
+        __hip_atomic_store(acc0 + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// Longest piece (in k-steps) the kernel is instantiated for.
+// Piece lengths (k-steps) the kernel is instantiated for.
 constexpr int kSkSteps[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
 
 template <int K>
 int gemv_sk_launch_k(int cb, int ns, const GemvSkParams& p, hipStream_t st) {
-    const size_t smem = gemv_sk_smem_bytes(p.m, ns);
+    const size_t smem = gemv_sk_smem_bytes(ns);
 #define EXL3_SK(CBV, NSV)                                                                              \
     if (cb == CBV && ns == NSV) {                                                                      \
         const void* fn = reinterpret_cast<const void*>(&gemv_sk_kernel<K, CBV, NSV>);                  \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 gemv");                                      \
         if (lrc) return lrc;                                                                           \
-        gemv_sk_kernel<K, CBV, NSV><<<p.nwg, SK_THREADS, smem, st>>>(p);                               \
+        gemv_sk_kernel<K, CBV, NSV><<<dim3(p.pieces, p.n / 128), SK_THREADS, smem, st>>>(p);          \
         return launch_status("exl3 gemv launch");                                                      \
     }
 #define EXL3_SK_CB(CBV)                                                                                \

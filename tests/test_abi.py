@@ -72,12 +72,12 @@ def _check_plan(m, k, n, K, experts=1):
     assert _lib.lib().exl3_gemv_plan(m, k, n, K, experts, out) == 0
     mb, ns, kw, splits, lds = list(out)
     assert 16 * mb >= m and 0 < lds <= 160 * 1024
-    balanced = experts == 1 and m <= 1 and m * n * 8 <= 4 * 1024 * 1024 and os.environ.get("EXL3_GEMV_SK") != "0"
+    balanced = experts == 1 and m == 1 and n * 8 <= 4 * 1024 * 1024 and os.environ.get("EXL3_GEMV_SK") != "0"
     if balanced:
-        # balanced kernel: each column block's k/64 k-steps in `splits` pieces of at most ns steps
+        # balanced bs=1 kernel: each column block's k/64 k-steps in `splits` equal pieces of ns steps
         ks_blk = k // 64
-        assert kw == 1 and 1 <= splits <= min(63, ks_blk)
-        assert ns == -(-ks_blk // splits) and ns in SK_STEPS
+        assert kw == 1 and 1 <= splits <= min(63, ks_blk) and ks_blk % splits == 0
+        assert ns == ks_blk // splits and ns in SK_STEPS
     else:
         # k-split kernel: k-slices covered exactly once, whole 128-row rotation blocks per workgroup
         assert 4 * ns * kw * splits == k // 16

@@ -172,28 +172,27 @@ def _with_env(env, fn):
                 os.environ[k] = v
 
 
-@pytest.mark.parametrize("m,k,n,K,cb,pieces", [
-    # k=512: 8 k-steps per column block cut into 3, 5 or 7 uneven pieces; every codebook
-    (1, 512, 384, 4, 1, 3), (1, 512, 384, 4, 1, 5), (2, 512, 384, 3, 2, 7), (5, 512, 384, 2, 0, 5),
-    (16, 512, 384, 4, 1, 1), (3, 768, 256, 5, 2, 2), (1, 256, 512, 3, 1, 4), (8, 1024, 256, 6, 1, 3),
-    (1, 2048, 128, 4, 1, 9), (4, 640, 640, 4, 2, 4), (1, 256, 256, 8, 0, 3), (1, 4096, 256, 4, 1, 63),
+@pytest.mark.parametrize("k,n,K,cb,pieces", [
+    # k/64 k-steps per column block in `pieces` equal pieces (1..16 steps each); every codebook,
+    # up to 64 contributions per output (the fixed-point accumulators' limit is 63: 32 is the max here)
+    (512, 384, 4, 1, 1), (512, 384, 4, 1, 2), (512, 384, 3, 2, 4), (512, 384, 2, 0, 8),
+    (768, 256, 5, 2, 2), (768, 256, 4, 1, 3), (768, 256, 4, 0, 4), (1024, 256, 6, 1, 16),
+    (2048, 128, 4, 1, 4), (640, 640, 4, 2, 10), (256, 256, 8, 0, 2), (4096, 256, 4, 1, 32),
+    (1792, 512, 3, 1, 4), (4096, 384, 1, 2, 16), (3072, 256, 7, 1, 12),
 ])
-def test_gemv_balanced_pieces(m, k, n, K, cb, pieces):
-    """Balanced kernel at forced piece counts: uneven pieces of each column block's k range,
-    up to the 63-contribution limit of the fixed-point accumulators, every codebook."""
-    print(f"case: balanced gemv m={m} k={k} n={n} K={K} cb={cb} pieces={pieces}", flush=True)
+def test_gemv_balanced_pieces(k, n, K, cb, pieces):
+    """Balanced bs=1 kernel at forced piece counts over every instantiated piece length."""
+    print(f"case: balanced gemv k={k} n={n} K={K} cb={cb} pieces={pieces}", flush=True)
     trellis, suh, svh = make_weight(k, n, K, seed=700 + pieces + 3 * K + cb)
-    x = make_x(m, k, seed=701 + m + pieces)
+    x = make_x(1, k, seed=701 + pieces)
     xd, tr, su, sv = to_dev(x, trellis, suh, svh)
-    ks_blk = k // 64
-    ns = -(-ks_blk // pieces)
-    env = {"EXL3_GEMV_SK_P": pieces, "EXL3_GEMV_SK_MAX_M": 16}  # the kernel serves m <= 16; the planner picks it for m = 1
-    plan = _with_env(env, lambda: _plan(m, k, n, K))
-    assert plan[1] == ns and plan[2] == 1 and plan[3] == pieces
+    env = {"EXL3_GEMV_SK_P": pieces}
+    plan = _with_env(env, lambda: _plan(1, k, n, K))
+    assert plan[1] == (k // 64) // pieces and plan[2] == 1 and plan[3] == pieces
     ys = [_with_env(env, lambda: _run_capi(xd, tr, su, sv, K, cb)) for _ in range(2)]
     torch.cuda.synchronize()
     ref = _oracle_ref(x, trellis, suh, svh, K, cb)
-    check_close(ys[0].float().cpu().numpy(), ref, f"balanced m={m} pieces={pieces}")
+    check_close(ys[0].float().cpu().numpy(), ref, f"balanced pieces={pieces}")
     # a second call on the same workspace gives the same bits (accumulators were cleared)
     assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
 
