@@ -101,6 +101,54 @@ __device__ __forceinline__ float sum_splits(const float* p, size_t stride, int S
     return sum;
 }
 
+// ------------------------------------------- fixed-point output accumulators
+//
+// Partial sums of one output element from several workgroups meet in a 64-bit
+// accumulator (zero between calls) through atomic adds that return the old
+// value; the add that completes the expected count finds the whole sum in the
+// returned value, so the hand-off costs one round trip and no separate
+// counter.  Integer addition is associative: the result does not depend on
+// the order in which contributions arrive.
+// Fixed-point format of the accumulators: value * 2^30 + 2^50 per
+// contribution in bits 0..57, contribution count in bits 58..63.
+constexpr int SK_CNT_SHIFT = 58;
+constexpr int SK_MAX_CONTRIB = 63;
+constexpr float SK_FX_SCALE = 1073741824.0f;  // 2^30
+constexpr float SK_FX_CLAMP = 1048576.0f;     // 2^20: above the fp16 range, so clamped values still give inf
+constexpr long long SK_FX_BIAS = 1ll << 50;   // 2^20 * 2^30: keeps every addend non-negative
+
+// One contribution: non-negative addend plus one count.  Non-finite partial
+// sums saturate to +-2^20 (NaN to +2^20) and so come out as +-inf.
+__device__ __forceinline__ unsigned long long sk_encode(float v) {
+    if (!(v == v)) v = SK_FX_CLAMP;
+    v = fminf(fmaxf(v, -SK_FX_CLAMP), SK_FX_CLAMP);
+    const long long q = (long long)rintf(v * SK_FX_SCALE);  // |q| <= 2^50, exact
+    return (unsigned long long)(q + SK_FX_BIAS) + (1ull << SK_CNT_SHIFT);
+}
+
+// Value of a completed accumulator holding `cnt` contributions.
+__device__ __forceinline__ float sk_decode(unsigned long long total, int cnt) {
+    const long long v = (long long)(total & ((1ull << SK_CNT_SHIFT) - 1)) - (long long)cnt * SK_FX_BIAS;
+    return (float)v * (1.0f / SK_FX_SCALE);
+}
+
+// Add a and b to the accumulators acc[0] and acc[1] (device scope); the add
+// that brings an element to `cnt` contributions stores it to y (fp16) and
+// clears the accumulator for the next call.
+__device__ __forceinline__ void fx_add_pair(unsigned long long* acc, float a, float b, int cnt, EXL3_GLOBAL __half* y) {
+    const unsigned long long ea = sk_encode(a), eb = sk_encode(b);
+    const unsigned long long oa = __hip_atomic_fetch_add(acc, ea, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long ob = __hip_atomic_fetch_add(acc + 1, eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((int)(oa >> SK_CNT_SHIFT) == cnt - 1) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y) = __half_as_ushort(__float2half_rn(sk_decode(oa + ea, cnt)));
+        __hip_atomic_store(acc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if ((int)(ob >> SK_CNT_SHIFT) == cnt - 1) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + 1) = __half_as_ushort(__float2half_rn(sk_decode(ob + eb, cnt)));
+        __hip_atomic_store(acc + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // Wait until this wave's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -26,28 +26,6 @@
 namespace exl3 {
 
 constexpr int SK_THREADS = 256;
-// Fixed-point format of the accumulators: value * 2^30 + 2^50 per
-// contribution in bits 0..57, contribution count in bits 58..63.
-constexpr int SK_CNT_SHIFT = 58;
-constexpr int SK_MAX_CONTRIB = 63;
-constexpr float SK_FX_SCALE = 1073741824.0f;  // 2^30
-constexpr float SK_FX_CLAMP = 1048576.0f;     // 2^20: above the fp16 range, so clamped values still give inf
-constexpr long long SK_FX_BIAS = 1ll << 50;   // 2^20 * 2^30: keeps every addend non-negative
-
-// One contribution: non-negative addend plus one count.  Non-finite partial
-// sums saturate to +-2^20 (NaN to +2^20) and so come out as +-inf.
-__device__ __forceinline__ unsigned long long sk_encode(float v) {
-    if (!(v == v)) v = SK_FX_CLAMP;
-    v = fminf(fmaxf(v, -SK_FX_CLAMP), SK_FX_CLAMP);
-    const long long q = (long long)rintf(v * SK_FX_SCALE);  // |q| <= 2^50, exact
-    return (unsigned long long)(q + SK_FX_BIAS) + (1ull << SK_CNT_SHIFT);
-}
-
-// Value of a completed accumulator holding `cnt` contributions.
-__device__ __forceinline__ float sk_decode(unsigned long long total, int cnt) {
-    const long long v = (long long)(total & ((1ull << SK_CNT_SHIFT) - 1)) - (long long)cnt * SK_FX_BIAS;
-    return (float)v * (1.0f / SK_FX_SCALE);
-}
 
 struct GemvSkParams {
     const __half* x;          // [k] (one row)
@@ -91,7 +69,6 @@ __device__ __forceinline__ void sk_frags(const uint32_t* buf, const uint32_t* mi
 template <int K, int CB, int NS>
 __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
     constexpr int D = gv_depth<K>();
-    constexpr int kts = 4 * NS;  // k-slices staged
     extern __shared__ __align__(16) unsigned char sk_smem[];
 
     const int n = p.n, P = p.pieces;
@@ -131,7 +108,9 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
     //    inside it, so its LDS slot is a per-lane constant plus 128 halves per
     //    local step.
     if (tid < 8) xs[NS * 128 + tid] = (_Float16)0.0f;
-    const int xs_lane = xs_index((2 * lane) & 63, 0, kts);
+    // xs_index((2 lane) % 64, 0, 4 NS) in closed form: k-tile (lane / 8) % 4,
+    // quarter lane % 4, value pair (lane / 4) % 2
+    const int xs_lane = ((lane >> 3) & 3) * 32 + (lane & 3) * 8 + ((lane >> 2) & 1) * 4;
     for (int jb = cw; jb < nblocks; jb += 4) {
         const int j = j0 + jb;
         const int l = 2 * j + (lane >> 5) - ks0;  // local step of this lane's values
@@ -143,11 +122,10 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
         fwht128_pair_f(a, c, lane);
         const _Float16 ha = (_Float16)(a * kHadNorm), hc = (_Float16)(c * kHadNorm);
         if (mine) {
-            const int ia = xs_lane + l * 128;
-            xs[ia] = ha;
-            xs[ia + 1] = ha;
-            xs[ia + 2] = hc;
-            xs[ia + 3] = hc;
+            // (ha, ha, hc, hc): the two values, each duplicated, in one 8-byte store
+            const uint32_t da = (uint32_t)__builtin_bit_cast(unsigned short, ha) * 0x10001u;
+            const uint32_t dc = (uint32_t)__builtin_bit_cast(unsigned short, hc) * 0x10001u;
+            *reinterpret_cast<uint2*>(xs + xs_lane + l * 128) = make_uint2(da, dc);
         }
         if constexpr (CB == 2) {
             // per-step sums over each half of the wave (lanes 0-31: k-step 2j, 32-63: 2j+1)
@@ -227,19 +205,7 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
     a = a * kHadNorm * __low2float(svv);
     b = b * kHadNorm * __high2float(svv);
     const int e0 = cb * 128 + 2 * lane;
-    unsigned long long* acc0 = p.acc + e0;
-    const unsigned long long ea = sk_encode(a), eb = sk_encode(b);
-    const unsigned long long oa = __hip_atomic_fetch_add(acc0, ea, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long ob = __hip_atomic_fetch_add(acc0 + 1, eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    EXL3_GLOBAL __half* y = gptr(p.y);
-    if ((int)(oa >> SK_CNT_SHIFT) == P - 1) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + e0) = __half_as_ushort(__float2half_rn(sk_decode(oa + ea, P)));
-        __hip_atomic_store(acc0, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if ((int)(ob >> SK_CNT_SHIFT) == P - 1) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + e0 + 1) = __half_as_ushort(__float2half_rn(sk_decode(ob + eb, P)));
-        __hip_atomic_store(acc0 + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    fx_add_pair(p.acc + e0, a, b, P, gptr(p.y) + e0);
 }
 
 // Piece lengths (k-steps) the kernel is instantiated for.
