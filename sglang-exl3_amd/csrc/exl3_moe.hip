@@ -91,6 +91,7 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int3
         if (tid == 63) {
             gptr(rt.counts)[0] = ia;
             gptr(rt.counts)[1] = iu;
+            gptr(rt.counts)[2] = ir;  // routed rows
         }
     }
     __syncthreads();
@@ -117,6 +118,32 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int3
             for (int j = 0; j < (int)(sizeof(MoeUnit) / 16); ++j) dst[j] = src[j];
         }
     }
+}
+
+// ------------------------------------------------------------------ rotation
+
+// Input rotation of the gate and up projections, once per routed row:
+// xr[p][crow] = fp16(FWHT(x[token] (.) suh_p[expert]) / sqrt(128)), p = 0 gate,
+// 1 up, rows by compact row.  The GEMV items then stage these rows as they
+// are, instead of rotating the same rows again for every column block they
+// cover.  One wave per (row, projection, 128-block); the operations are the
+// GEMV staging's, so the staged values are the same.
+__global__ __launch_bounds__(256) void moe_rotate_kernel(const __half* x, const int32_t* ids, MoeTables tabs,
+                                                         MoeRoute rt, int topk, int entries, int hidden,
+                                                         __half* xr) {
+    const int nblk = hidden >> 7, per_row = 2 * nblk;
+    const int job = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int crow = job / per_row;
+    if (crow >= gptr(rt.counts)[2]) return;
+    const int rem = job - crow * per_row, proj = rem / nblk, j = rem - proj * nblk;
+    const int entry = gptr(rt.rows)[crow];
+    const int e = gptr(ids)[entry];
+    const __half* suh = reinterpret_cast<const __half*>(gptr(tabs.t[proj == 0 ? 1 : 4])[e]);
+    const int kg = j * 128 + 2 * lane;
+    const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)(entry / topk) * hidden + kg), ld_h2(gptr(suh) + kg));
+    float a = __low2float(pr), c = __high2float(pr);
+    fwht128_pair_f(a, c, lane);
+    st_h2(gptr(xr) + ((size_t)proj * entries + crow) * hidden + kg, __floats2half2_rn(a * kHadNorm, c * kHadNorm));
 }
 
 // ------------------------------------------------------------------ combine
@@ -261,10 +288,16 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
     return MoePlan{ns, kw, S, bpi};
 }
 
+// Batches of at least this many tokens rotate the gate/up input rows once in a
+// pass of their own (moe_rotate_kernel); below it each GEMV item rotates its
+// rows (one row per unit at one token: nothing to share).
+constexpr int kMoeRotTokens = 8;
+
 struct MoeLayout {
     int entries, max_units;
+    bool rot;
     MoePlan gu, dn;
-    size_t route_off, units_off, rows_off, h_off, y_off, part_off, total;
+    size_t route_off, units_off, rows_off, h_off, y_off, xr_off, part_off, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -281,7 +314,7 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     L.dn = plan_moe(units, L.entries, inter, hidden, 1);
     size_t o = kWsScratchOffset;
     L.route_off = o;
-    o = align256(o + 2 * sizeof(int));
+    o = align256(o + 4 * sizeof(int));
     L.units_off = o;
     o = align256(o + (size_t)L.max_units * sizeof(MoeUnit));
     L.rows_off = o;
@@ -290,6 +323,9 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     o = align256(o + (size_t)L.entries * inter * 2);
     L.y_off = o;
     o = align256(o + (size_t)L.entries * hidden * 2);
+    L.rot = tokens >= env_int("EXL3_MOE_ROT_TOKENS", kMoeRotTokens);
+    L.xr_off = o;
+    if (L.rot) o = align256(o + (size_t)2 * L.entries * hidden * 2);
     L.part_off = o;
     const size_t pg = (size_t)(inter / 128) * 2 * L.gu.splits;
     const size_t pd = (size_t)(hidden / 128) * 1 * L.dn.splits;
@@ -349,9 +385,20 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     p.counters = reinterpret_cast<int*>(w8);
     p.partials = reinterpret_cast<float*>(w8 + L.part_off);
 
-    // 2. gate + up (+ SwiGLU + down input rotation)
+    // 2. gate/up input rotation, once per routed row (larger batches)
+    __half* xr = reinterpret_cast<__half*>(w8 + L.xr_off);
+    if (L.rot) {
+        const long long jobs = (long long)L.entries * 2 * (hidden / 128);
+        moe_rotate_kernel<<<(unsigned)((jobs + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x), ids, tb, rt,
+                                                                      topk, L.entries, hidden, xr);
+        const int rc = launch_status("exl3 moe rotate launch");
+        if (rc) return rc;
+    }
+
+    // 3. gate + up (+ SwiGLU + down input rotation)
     p.mode = MOE_GATE_UP;
-    p.x = reinterpret_cast<const __half*>(x);
+    p.x = L.rot ? xr : reinterpret_cast<const __half*>(x);
+    p.in_rot = L.rot;
     p.out = h;
     p.k = hidden;
     p.n = inter;
@@ -375,8 +422,9 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
         if (rc) return rc;
     }
 
-    // 3. down
+    // 4. down
     p.mode = MOE_DOWN;
+    p.in_rot = 0;
     p.x = h;
     p.out = yslots;
     p.k = inter;
@@ -390,7 +438,7 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     rc = moe_launch(KD, cb, L.dn.ns, p, st);
     if (rc) return rc;
 
-    // 4. weighted combine
+    // 5. weighted combine
     moe_combine_kernel<<<dim3((hidden / 2 + 255) / 256, tokens), 256, 0, st>>>(
         yslots, ids, weights, weights_f16, topk, E, hidden, reinterpret_cast<__half*>(out));
     return launch_status("exl3 moe combine launch");

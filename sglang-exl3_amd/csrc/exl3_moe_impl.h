@@ -31,6 +31,10 @@ namespace exl3 {
 
 constexpr int MOE_GATE_UP = 0;
 constexpr int MOE_DOWN = 1;
+// Kernel variants (compile-time, so each holds only its own code path):
+constexpr int MV_GU = 0;      // gate/up, input rows rotated by each item
+constexpr int MV_GU_ROT = 1;  // gate/up, input rows arrive rotated per projection
+constexpr int MV_DOWN = 2;    // down, input rows arrive rotated
 constexpr int MOE_ROUTE_THREADS = 1024;
 constexpr int MOE_UNIT_ROWS = 16;  // rows of a work unit: one MFMA row block
 constexpr int MV_PRE = 2;          // rotation blocks per wave whose activations are preloaded
@@ -73,6 +77,8 @@ struct MoeParams {
     int kw;            // k waves per workgroup
     int bx_per_item;   // column blocks one item covers (divides n/128)
     int mode;
+    int in_rot;        // GATE_UP: x holds the rows already rotated per projection,
+                       // [2][entries][k] by compact row (moe_rotate_kernel)
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries) { return (size_t)(3 * E + entries) * sizeof(int); }
@@ -101,7 +107,7 @@ __device__ __forceinline__ __half2 ld_h2_ptr(const void* base, int idx) {
 // arrives rotated), decode + MFMA the split's k range for 128 columns, store
 // fp32 partial rows; the last of nproj * S arrivals of (unit, column block)
 // runs the epilogue.
-template <int K, int CB, int NS>
+template <int K, int CB, int NS, int MODE>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
     constexpr int ROWS = MOE_UNIT_ROWS;
     extern __shared__ __align__(16) unsigned char mv_smem[];
@@ -123,7 +129,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cw = wave & 3, kwi = wave >> 2;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
-    const bool pre_rotated = p.mode == MOE_DOWN;
+    constexpr bool down = MODE == MV_DOWN;
+    constexpr bool pre_rotated = MODE != MV_GU;  // input rows arrive rotated
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const size_t split_stride = (size_t)p.entries * 128;
 
@@ -145,10 +152,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
 
         const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
         const int m = uniform_i(ud->nrows), crow0 = uniform_i(ud->crow0);
-        const int pb = pre_rotated ? 6 : 3 * proj;
+        const int pb = down ? 6 : 3 * proj;
         const uint32_t* trellis = reinterpret_cast<const uint32_t*>(uniform_p(ud->ptr[pb]));
         const void* suh = uniform_p(ud->ptr[pb + 1]);
-        const void* ev0p = uniform_p(ud->ptr[pre_rotated ? 8 : 2]);  // svh of down / gate
+        const void* ev0p = uniform_p(ud->ptr[down ? 8 : 2]);  // svh of down / gate
         const void* ev1p = uniform_p(ud->ptr[5]);                    // svh of up
         const void* ev2p = uniform_p(ud->ptr[7]);                    // suh of down (its input rotation)
         const int kt_wg0 = sidx * kts_wg;
@@ -160,7 +167,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
         if (it != (int)blockIdx.x) __syncthreads();  // the previous item is done with LDS
 
         auto x_row = [&](int row) -> const EXL3_GLOBAL __half* {
-            if (pre_rotated) return gptr(p.x) + (size_t)(crow0 + row) * k;
+            if (pre_rotated) return gptr(p.x) + ((size_t)(down ? 0 : proj * p.entries) + crow0 + row) * k;
             if (p.single_token) return gptr(p.x);
             return gptr(p.x) + (size_t)(rows_g[crow0 + row] / p.topk) * k;
         };
@@ -234,7 +241,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
             const int c0 = bx * 128 + 2 * lane;
             const __half2 ev0 = ld_h2_ptr(ev0p, c0);
             __half2 ev1 = __half2{}, ev2 = __half2{};
-            if (!pre_rotated) {
+            if (!down) {
                 ev1 = ld_h2_ptr(ev1p, c0);
                 ev2 = ld_h2_ptr(ev2p, c0);
             }
@@ -308,7 +315,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                 }
             };
             EXL3_GLOBAL __half* outg = gptr(p.out);
-            if (!pre_rotated) {
+            if (!down) {
                 const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
                 for (int row = wave; row < m; row += nwaves) {
                     const int crow = crow0 + row;
@@ -366,19 +373,23 @@ template <int K>
 int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     const size_t smem = moe_smem_bytes(4 * ns * p.kw, p.kw);
     const int threads = 256 * p.kw;
-#define EXL3_MV_NS(CBV, NSV)                                                                           \
-    if (cb == CBV && ns == NSV) {                                                                      \
-        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV>);                 \
+    const int mv = p.mode == MOE_DOWN ? MV_DOWN : (p.in_rot ? MV_GU_ROT : MV_GU);
+#define EXL3_MV_NS(CBV, NSV, MVV)                                                                      \
+    if (cb == CBV && ns == NSV && mv == MVV) {                                                         \
+        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV>);            \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe");                                       \
         if (lrc) return lrc;                                                                           \
         const int grid = moe_grid_size(fn, threads, smem);                                             \
         if (grid <= 0) return EXL3_ERR_HIP;                                                            \
-        moe_gemv_kernel<K, CBV, NSV><<<grid, threads, smem, st>>>(p);                                  \
+        moe_gemv_kernel<K, CBV, NSV, MVV><<<grid, threads, smem, st>>>(p);                             \
         return launch_status("exl3 moe launch");                                                      \
     }
-#define EXL3_MV_CASE(CBV) EXL3_MV_NS(CBV, 2) EXL3_MV_NS(CBV, 4) EXL3_MV_NS(CBV, 8) EXL3_MV_NS(CBV, 16)
+#define EXL3_MV_MODES(CBV, NSV) EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)
+#define EXL3_MV_CASE(CBV) \
+    EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 16)
     EXL3_MV_CASE(0) EXL3_MV_CASE(1) EXL3_MV_CASE(2)
 #undef EXL3_MV_CASE
+#undef EXL3_MV_MODES
 #undef EXL3_MV_NS
     set_error("exl3 moe: no kernel for codebook %d steps %d", cb, ns);
     return EXL3_ERR_UNSUPPORTED;

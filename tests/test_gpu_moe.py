@@ -216,6 +216,21 @@ def test_moe_cfg4_batch16():
     check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), "moe cfg4 B=16")
 
 
+@pytest.mark.parametrize("T,topk,E,cb,invalid", [(2, 4, 8, 1, 0), (9, 4, 8, 2, 3), (33, 2, 4, 1, 0), (12, 6, 16, 0, 2)])
+@pytest.mark.parametrize("rot_tokens", [1, 100000])
+def test_moe_rotation_pass(T, topk, E, cb, invalid, rot_tokens, monkeypatch):
+    """Gate/up input rows rotated once per call in a pass of their own (threshold 1) or by every
+    GEMV item (threshold above T): both against the oracle, with skipped slots."""
+    print(f"case: moe rotation pass T={T} topk={topk} E={E} cb={cb} rot_tokens={rot_tokens}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_ROT_TOKENS", str(rot_tokens))
+    ex = Experts(E, 512, 256, (3, 3, 3), cb, seed=80 + T + E)
+    x = make_x(T, 512, seed=81 + T)
+    ids, w = _routing(T, topk, E, seed=82 + T, invalid=invalid)
+    out = _layer_capi(ex, x, ids, w, cb=cb)
+    torch.cuda.synchronize()
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), f"moe rotation pass T={T}")
+
+
 def test_moe_rejects_bad_arguments():
     ex = Experts(2, 256, 128, (2, 2, 2), 1, seed=1)
     x = torch.zeros((1, 200), dtype=torch.float16, device="cuda")
