@@ -61,14 +61,27 @@ struct FatPlan {
     int mt, splits;
 };
 
-// Rows per tile from M; k-splits until the grid holds ~4 workgroups per CU
-// (each split's steps must be whole chunks of FAT_CH, except a lone tail).
+// Wide tiles (128 x 256, fat_big_kernel) from kFatWideRows rows on (env
+// EXL3_FAT_WIDE=0 turns them off); below, rows per tile from M.  k-splits until
+// the grid fills the chip: ~4 workgroups per CU for the narrow kernel (each
+// split a whole number of FAT_CH chunks), 2 per CU for the wide one (an even
+// number of steps per split).
+constexpr int kFatWideRows = 65;
+
 FatPlan plan_fat(int M, int k, int n) {
     FatPlan pl;
-    pl.mt = M >= 128 ? 128 : (M > 16 ? 64 : 16);
-    const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
     const int ksteps = k / 64;
     pl.splits = 1;
+    const char* env = getenv("EXL3_FAT_WIDE");
+    const bool wide_on = !(env && env[0] == '0');
+    if (wide_on && M >= kFatWideRows && n % FB_COLS == 0) {
+        pl.mt = FAT_MT_WIDE;
+        const long long base = (long long)(n / FB_COLS) * ((M + FB_ROWS - 1) / FB_ROWS);
+        while (base * pl.splits < 512 && pl.splits < 16 && ksteps % (4 * pl.splits) == 0) pl.splits *= 2;
+        return pl;
+    }
+    pl.mt = M >= 128 ? 128 : (M > 16 ? 64 : 16);
+    const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
     while (base * pl.splits < 1024 && pl.splits < 16 && ksteps % (2 * pl.splits) == 0 &&
            (ksteps / (2 * pl.splits)) % FAT_CH == 0)
         pl.splits *= 2;

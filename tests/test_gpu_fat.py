@@ -56,6 +56,70 @@ def test_fat_gemm_vs_oracle(M, k, n, K, cb):
     check_close(out.cpu().numpy(), _ref(a, tr, sv, K, cb), f"fat M={M}")
 
 
+def _with_env(name, value, fn):
+    import os
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        return fn()
+    finally:
+        if old is None:
+            del os.environ[name]
+        else:
+            os.environ[name] = old
+
+
+def _fat(a, tr, sv, K, cb, M, n):
+    out = torch.full((M, n), 123.0, dtype=torch.float32, device="cuda")  # overwritten
+    torch.ops.sglang_exl3.exl3_fat_gemm(torch.from_numpy(a).cuda(), torch.from_numpy(tr).cuda(), out,
+                                        torch.from_numpy(sv).cuda(), K, cb == 1, cb == 2)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_fat_wide_tiles_every_width(K, cb):
+    """Wide-tile kernel (128 x 256 tiles, from 65 rows): every bit width and codebook,
+    a partial second row tile, two k-splits accumulating atomically."""
+    M, k, n = 130, 256, 256
+    print(f"case: fat wide M={M} k={k} n={n} K={K} cb={cb}", flush=True)
+    tr, su, sv = make_weight(k, n, K, seed=100 + 3 * K + cb)
+    a = _rotate(make_x(M, k, seed=K + 10 * cb), su)
+    check_close(_fat(a, tr, sv, K, cb, M, n), _ref(a, tr, sv, K, cb), f"fat wide K={K} cb={cb}")
+
+
+@pytest.mark.parametrize("M,k,n,K,cb", [(512, 1024, 512, 3, 2), (257, 512, 768, 4, 1), (65, 2048, 256, 2, 0),
+                                        (1100, 128, 512, 5, 1)])
+@pytest.mark.parametrize("wide", ["1", "0"])
+def test_fat_wide_and_narrow_kernels(M, k, n, K, cb, wide):
+    """The same shapes through the wide-tile kernel and the narrow one (EXL3_FAT_WIDE=0)."""
+    print(f"case: fat M={M} k={k} n={n} K={K} cb={cb} wide={wide}", flush=True)
+    tr, su, sv = make_weight(k, n, K, seed=M + n)
+    a = _rotate(make_x(M, k, seed=M + 1), su)
+    out = _with_env("EXL3_FAT_WIDE", wide, lambda: _fat(a, tr, sv, K, cb, M, n))
+    check_close(out, _ref(a, tr, sv, K, cb), f"fat M={M} wide={wide}")
+
+
+def test_fat_wide_scatter_accumulates():
+    M, k, n, K = 150, 512, 512, 3
+    tr, su, sv = make_weight(k, n, K, seed=15)
+    a = _rotate(make_x(M, k, seed=16), su)
+    rng = np.random.default_rng(17)
+    tok = rng.integers(0, 40, size=M).astype(np.int64)
+    rw = (rng.random(M) + 0.5).astype(np.float16)
+    base = rng.standard_normal((40, n)).astype(np.float32)
+    out = torch.from_numpy(base.copy()).cuda()
+    torch.ops.sglang_exl3.exl3_fat_gemm_scatter(torch.from_numpy(a).cuda(), torch.from_numpy(tr).cuda(), out,
+                                                torch.from_numpy(sv).cuda(), torch.from_numpy(tok).cuda(),
+                                                torch.from_numpy(rw).cuda(), K, False, True)
+    torch.cuda.synchronize()
+    rows = _ref(a, tr, sv, K, 2) * rw.astype(np.float32)[:, None]
+    want = base.copy()
+    np.add.at(want, tok, rows)
+    check_close(out.cpu().numpy() - base, want - base, "fat wide scatter")
+
+
 def test_fat_gemm_scatter_accumulates():
     M, k, n, K = 48, 256, 256, 4
     tr, su, sv = make_weight(k, n, K, seed=5)
@@ -76,7 +140,8 @@ def test_fat_gemm_scatter_accumulates():
     check_close(out.cpu().numpy() - base, want - base, "fat scatter")
 
 
-@pytest.mark.parametrize("m,k,n,K,cb", [(65, 256, 256, 4, 1), (200, 512, 384, 3, 2), (1000, 256, 128, 2, 1)])
+@pytest.mark.parametrize("m,k,n,K,cb", [(65, 256, 256, 4, 1), (200, 512, 384, 3, 2), (1000, 256, 128, 2, 1),
+                                        (300, 128, 512, 3, 1), (700, 1024, 256, 4, 2)])
 def test_gemm_prefill_path_vs_oracle(m, k, n, K, cb):
     print(f"case: gemm prefill m={m} k={k} n={n}", flush=True)
     tr, su, sv = make_weight(k, n, K, seed=m + k)
