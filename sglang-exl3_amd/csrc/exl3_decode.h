@@ -103,6 +103,33 @@ __device__ __forceinline__ void fwht128_pair_f(float& a, float& b, int lane) {
     fwht_stage<32>(a, b, lane);
 }
 
+// The same transform with one row held as 16 consecutive values per lane over
+// 8 lanes (value 16 (lane & 7) + e in v[e]): stages of stride 1 .. 8 in
+// registers, 16 .. 64 across the lanes (xor 1, 2, 4), in the same order and
+// with the same float operations as fwht128_pair_f (x + y below, x - y above;
+// fma(v, -1, p) is p - v exactly).
+template <int J>
+__device__ __forceinline__ void fwht_x16_stage(float (&v)[16], int lane) {
+    const float sg = (lane & J) ? -1.f : 1.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = __builtin_fmaf(v[e], sg, lane_xor<J>(v[e]));
+}
+
+__device__ __forceinline__ void fwht128_x16(float (&v)[16], int lane) {
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            if (!(e & h)) {
+                const float x = v[e], y = v[e | h];
+                v[e] = x + y;
+                v[e | h] = x - y;
+            }
+    fwht_x16_stage<1>(v, lane);
+    fwht_x16_stage<2>(v, lane);
+    fwht_x16_stage<4>(v, lane);
+}
+
 // Sum of v over the 64 lanes of the wave (every lane gets the same total,
 // accumulated in a fixed order).
 __device__ __forceinline__ float wave_sum(float v) {

@@ -61,11 +61,13 @@ struct FatPlan {
     int mt, splits;
 };
 
-// Wide tiles (128 x 256, fat_big_kernel) from kFatWideRows rows on (env
+// Wide tiles (256 x 256, fat_big_kernel) from kFatWideRows rows on (env
 // EXL3_FAT_WIDE=0 turns them off); below, rows per tile from M.  k-splits until
 // the grid fills the chip: ~4 workgroups per CU for the narrow kernel (each
-// split a whole number of FAT_CH chunks), 2 per CU for the wide one (an even
-// number of steps per split).
+// split a whole number of FAT_CH chunks).  The wide kernel splits only grids
+// under 96 workgroups (an even number of steps per split): its outputs are
+// large, and split outputs cost a zero fill plus one fp32 atomic per value
+// and split, which measured slower than leaving up to 60 % of the CUs idle.
 constexpr int kFatWideRows = 65;
 
 FatPlan plan_fat(int M, int k, int n) {
@@ -77,7 +79,7 @@ FatPlan plan_fat(int M, int k, int n) {
     if (wide_on && M >= kFatWideRows && n % FB_COLS == 0) {
         pl.mt = FAT_MT_WIDE;
         const long long base = (long long)(n / FB_COLS) * ((M + FB_ROWS - 1) / FB_ROWS);
-        while (base * pl.splits < 512 && pl.splits < 16 && ksteps % (4 * pl.splits) == 0) pl.splits *= 2;
+        while (base * pl.splits < 96 && pl.splits < 16 && ksteps % (4 * pl.splits) == 0) pl.splits *= 2;
         return pl;
     }
     pl.mt = M >= 128 ? 128 : (M > 16 ? 64 : 16);

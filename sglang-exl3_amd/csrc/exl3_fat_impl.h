@@ -181,33 +181,43 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
 
 // ------------------------------------------------------------ wide tiles
 //
-// MFMA-bound shapes (many rows).  A workgroup of 4 waves owns 128 rows x 256
-// columns; each wave 64 columns (two 32-value decode groups per lane) times
-// all 128 rows, so each staged A fragment feeds four MFMAs and each decoded
-// weight 128 rows.  Two workgroups share a CU (<= 256 registers per lane), so
-// one wave's decode (VALU) runs beside the other's MFMAs.
+// MFMA-bound shapes (many rows).  A workgroup of 8 waves owns 256 rows x 256
+// columns: wave (rh, cq) computes rows 128rh .. +128 x columns 64cq .. +64
+// (row blocks x two 32-column decode groups per lane).  The two waves of a
+// column quarter share its decode: wave rh decodes group G = rh of the next
+// step and posts the MFMA B fragments in LDS; both read both groups back.  So
+// each decoded weight feeds 256 rows at half a 64-column decode per wave, and
+// each staged A fragment feeds four MFMAs.  Two waves per SIMD, 128
+// accumulators each.  (On gfx950 VALU and MFMA work barely overlap: the
+// decode's VALU time adds to the MFMA time, so it is cut per MAC.)
 //
-// A is staged one step (64 k) at a time into two LDS buffers by direct
-// global->LDS loads (global_load_lds_dwordx4: lane l writes bytes
-// [16l, 16l+16) of the instruction's 1 KB), in natural k order with the
-// 16-byte chunk index XOR-swizzled by row (chunk ^ (row & 7) ^ ((row >> 3) & 1)),
-// which keeps the fragment reads conflict-free for 8- and 16-lane LDS phases.
-// Natural k order works because each lane decodes all 16 k values of its two
-// columns: fragment word j of run h' is tile rows (8h' + 2j, 8h' + 2j + 1).
+// A is staged one step (64 k) at a time into two LDS buffers: each thread
+// loads four 16-byte chunks of the next step into registers after its decode
+// and writes them after its MFMAs, in natural k order with the 16-byte chunk
+// index XOR-swizzled by row (chunk ^ (row & 7) ^ ((row >> 3) & 1)), which
+// keeps the fragment reads conflict-free for 8- and 16-lane LDS phases.
+// (Direct global->LDS loads measured slower, and the compiler's vmcnt
+// tracking does not see them, forcing full waits.)  Natural k order works
+// because each lane decodes all 16 k values of its two columns: fragment word
+// j of run h' is tile rows (8h' + 2j, 8h' + 2j + 1).  B fragments sit
+// chunk-major ([quarter][group][chunk][lane] x 16 bytes), so their 16-byte
+// writes and reads are conflict-free too.
 //
-// Step s: stage A of step s+1 into the other buffer, decode step s, request
-// the weights of step s+1 into the registers just decoded, run the step's 64
-// MFMAs; one barrier per step (its vmcnt(0) lands both requests).
-constexpr int FB_ROWS = 128;
-constexpr int FB_COLS = 256;                  // 4 waves x 64 columns
-constexpr int FB_THREADS = 256;
-constexpr int FB_STEP_BYTES = FB_ROWS * 128;  // 128 rows x 64 k fp16
-constexpr int FB_PASS_ROWS = 32;              // epilogue rows per LDS pass
-constexpr int FB_CTS = FB_COLS + 4;           // epilogue row stride (floats)
-constexpr int FAT_MT_WIDE = 0;                // plan value (rows per tile) selecting fat_big_kernel
+// Step s: decode this wave's group of step s+1 into the other B buffer,
+// request the weights of step s+2 and the A chunks of step s+1, run the
+// step's 64 MFMAs on the current buffers, write the A chunks; one barrier per
+// step, which waits for the LDS traffic only.
+constexpr int FB_ROWS = 256;
+constexpr int FB_COLS = 256;
+constexpr int FB_THREADS = 512;                 // 8 waves: 2 row halves x 4 column quarters
+constexpr int FB_A_BYTES = FB_ROWS * 128;       // one staged step: 256 rows x 64 k fp16
+constexpr int FB_B_BYTES = 4 * 2 * 4 * 64 * 16;  // one step's B fragments: [quarter][group][chunk][lane]
+constexpr int FB_PASS_ROWS = 64;                // epilogue rows per LDS pass (32 of each half)
+constexpr int FB_CTS = FB_COLS + 4;             // epilogue row stride (floats)
+constexpr int FAT_MT_WIDE = 0;                  // plan value (rows per tile) selecting fat_big_kernel
 
 constexpr size_t fat_big_smem_bytes() {
-    constexpr size_t stage = 2 * (size_t)FB_STEP_BYTES;
+    constexpr size_t stage = 2 * (size_t)FB_A_BYTES + 2 * (size_t)FB_B_BYTES;
     constexpr size_t tile = (size_t)FB_PASS_ROWS * FB_CTS * sizeof(float);
     return stage > tile ? stage : tile;
 }
@@ -249,52 +259,58 @@ __device__ __forceinline__ void nat_group(const uint32_t (&w)[K], int prev_addr,
 
 template <int K, int CB>
 __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
-    constexpr int RB = FB_ROWS / 16;
-    constexpr int LOADS = FB_STEP_BYTES / 1024 / (FB_THREADS / 64);  // 1 KB direct loads per wave per step
-    static_assert(LOADS % 2 == 0, "the row-parity swizzle bit must be static per load");
+    constexpr int RB = FB_ROWS / 2 / 16;  // row blocks per wave
+    static_assert(FB_A_BYTES == 4 * 16 * FB_THREADS, "four 16-byte A chunks per thread and step");
     extern __shared__ __align__(16) unsigned char fat_smem[];
+    unsigned char* const bsm = fat_smem + 2 * FB_A_BYTES;
 
     const int bx = blockIdx.x, sidx = blockIdx.z;
     const int m0 = blockIdx.y * FB_ROWS;
     const int rows = min(FB_ROWS, p.M - m0);
-    const int tid = threadIdx.x, cw = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int rh = wv >> 2, cq = wv & 3;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
     const int ntiles = p.n >> 4;
     const int nsteps = p.ksteps;  // even
     const int kt0 = sidx * nsteps * 4;
-    const int nt0 = bx * (FB_COLS / 16) + cw * 4 + (i >> 3);  // group G adds 2G tiles
-    const EXL3_GLOBAL uint32_t* tb = gptr(p.trellis) + ((size_t)(kt0 + g) * ntiles + nt0) * (8 * K) + K * q;
+    // this wave decodes group rh of quarter cq: column tiles 4cq + 2rh + (i >> 3)
+    const int nt = bx * (FB_COLS / 16) + cq * 4 + rh * 2 + (i >> 3);
+    const EXL3_GLOBAL uint32_t* tb = gptr(p.trellis) + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
 
-    // direct-load sources: load j of this wave fills LDS rows 8J .. 8J+7
-    // (J = cw*LOADS + j); lane l writes row 8J + (l >> 3), physical chunk l & 7,
-    // which holds logical chunk (l & 7) ^ (l >> 3) ^ (J & 1).  Rows past M
-    // repeat the last row (their results are never stored).
+    // A staging: thread t moves chunks u = t + 512j (j < 4): tile row u >> 3,
+    // physical chunk u & 7, which holds logical chunk (u & 7) ^ (row & 7) ^
+    // ((row >> 3) & 1).  Rows past M repeat the last row (never stored).
     const EXL3_GLOBAL char* abase =
         reinterpret_cast<const EXL3_GLOBAL char*>(gptr(p.a)) + ((size_t)m0 * p.k + (size_t)kt0 * 16) * 2;
-    uint32_t aoff[LOADS];
+    uint32_t aoff[4];
 #pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        const int J = cw * LOADS + j;
-        const int row = min(8 * J + (lane >> 3), rows - 1);
-        const int c = (lane & 7) ^ (lane >> 3) ^ (j & 1);
+    for (int j = 0; j < 4; ++j) {
+        const int u = tid + FB_THREADS * j;
+        const int row = min(u >> 3, rows - 1);
+        const int c = (u & 7) ^ ((u >> 3) & 7) ^ ((u >> 6) & 1);
         aoff[j] = (uint32_t)row * (uint32_t)p.k * 2u + 16u * (uint32_t)c;
     }
-    auto stage_a = [&](int step, int bufi) {
+    u32x4_t areg[4];
+    auto load_a = [&](int step) {
         const EXL3_GLOBAL char* src = abase + (size_t)step * 128;
 #pragma unroll
-        for (int j = 0; j < LOADS; ++j)
-            __builtin_amdgcn_global_load_lds(
-                reinterpret_cast<const EXL3_GLOBAL void*>(src + aoff[j]),
-                (__attribute__((address_space(3))) void*)(fat_smem + (size_t)bufi * FB_STEP_BYTES +
-                                                          (size_t)(cw * LOADS + j) * 1024),
-                16, 0, 0);
+        for (int j = 0; j < 4; ++j) areg[j] = *reinterpret_cast<const EXL3_GLOBAL u32x4_t*>(src + aoff[j]);
     };
-    // fragment reads: row 16rb + i, logical chunk 2g + h'
+    auto write_a = [&](int bufi) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<u32x4_t*>(fat_smem + (size_t)bufi * FB_A_BYTES + (size_t)(tid + FB_THREADS * j) * 16) =
+                areg[j];
+    };
+    // A fragment reads: row 128rh + 16rb + i, logical chunk 2g + h'
     uint32_t rd_off[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) rd_off[h] = (uint32_t)i * 128u + 16u * (uint32_t)((2 * g + h) ^ (i & 7) ^ (i >> 3));
+    for (int h = 0; h < 2; ++h)
+        rd_off[h] = (uint32_t)(rh * 128 + i) * 128u + 16u * (uint32_t)((2 * g + h) ^ (i & 7) ^ (i >> 3));
+    // B fragments: chunk (c, h') of group G of this quarter
+    auto b_off = [&](int G, int c, int h) { return (uint32_t)(((cq * 2 + G) * 4 + c * 2 + h) * 1024 + lane * 16); };
 
     float4_t acc[RB][2][2];  // [row block][group][column half]
 #pragma unroll
@@ -304,102 +320,167 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[rb][G][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    uint32_t w[2][K];  // [group][word] of the current step
-    auto load_step = [&](int step) {
-        const EXL3_GLOBAL uint32_t* t = tb + (size_t)step * step_stride;
-        load_words<K>(t, w[0]);
-        load_words<K>(t + 16 * K, w[1]);
+    uint32_t w[K];  // this wave's words of the next step to decode
+    auto load_step = [&](int step) { load_words<K>(tb + (size_t)step * step_stride, w); };
+    auto decode_post = [&](int bufi) {
+        uint32_t fr[2][2][4];  // [column half][h'][j]
+        nat_group<K, CB>(w, prev_addr, fr);
+        unsigned char* bb = bsm + (size_t)bufi * FB_B_BYTES;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                *reinterpret_cast<u32x4_t*>(bb + b_off(rh, c, h)) = u32x4_t{fr[c][h][0], fr[c][h][1], fr[c][h][2], fr[c][h][3]};
     };
+
     load_step(0);
-    stage_a(0, 0);
+    load_a(0);
+    write_a(0);
+    __syncthreads();
+    decode_post(0);
+    load_step(nsteps > 1 ? 1 : 0);
     __syncthreads();
 
-    // buffer SL = s & 1 holds step s's staged A; requests past the last step are
-    // clamped to it (no branch inside the unrolled body)
-    auto step_body = [&](int s, auto slot_c) {
+    // buffers SL = s & 1 hold step s; requests past the last step are clamped
+    // to it (no branch inside the unrolled body; the extra decode is unused)
+    auto mfma_phase = [&](auto slot_c) {
         constexpr int SL = decltype(slot_c)::value;
-        const int next = s + 1 < nsteps ? s + 1 : s;
-        stage_a(next, SL ^ 1);
-        uint32_t fr[2][2][2][4];  // [group][column half][h'][j]
-        nat_group<K, CB>(w[0], prev_addr, fr[0]);
-        nat_group<K, CB>(w[1], prev_addr, fr[1]);
-        load_step(next);
-        // keep the decode and the MFMA phase apart: mixing them raises register
-        // pressure past the 256 of two waves per SIMD (spills for some K)
-        __builtin_amdgcn_sched_barrier(0);
-        const unsigned char* buf = fat_smem + (size_t)SL * FB_STEP_BYTES;
+        const unsigned char* ab = fat_smem + (size_t)SL * FB_A_BYTES;
+        const unsigned char* bb = bsm + (size_t)SL * FB_B_BYTES;
+        half8_t B[2][2][2];  // [group][column half][h']
+#pragma unroll
+        for (int G = 0; G < 2; ++G)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) B[G][c][h] = *reinterpret_cast<const half8_t*>(bb + b_off(G, c, h));
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const half8_t A = *reinterpret_cast<const half8_t*>(buf + rd_off[h] + rb * 2048);
+                const half8_t A = *reinterpret_cast<const half8_t*>(ab + rd_off[h] + rb * 2048);
 #pragma unroll
                 for (int G = 0; G < 2; ++G)
 #pragma unroll
                     for (int c = 0; c < 2; ++c)
-                        acc[rb][G][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            A, *reinterpret_cast<const half8_t*>(fr[G][c][h]), acc[rb][G][c], 0, 0, 0);
+                        acc[rb][G][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[G][c][h], acc[rb][G][c], 0, 0, 0);
             }
         }
-        __syncthreads();
+    };
+    // The decode and MFMA phases are kept apart (sched_barrier): mixing them
+    // raises register pressure past the 256 of two waves per SIMD.
+    auto step_body = [&](int s, auto slot_c) {
+        constexpr int SL = decltype(slot_c)::value;
+        const int n1 = s + 1 < nsteps ? s + 1 : s;
+        const int n2 = s + 2 < nsteps ? s + 2 : n1;
+        decode_post(SL ^ 1);
+        load_step(n2);
+        load_a(n1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_phase(slot_c);
+        __builtin_amdgcn_sched_barrier(0);
+        write_a(SL ^ 1);
+        // A barrier on the LDS traffic only (__syncthreads would also wait for
+        // the weight request, which the next decode waits for by itself).
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     };
     for (int s = 0; s < nsteps; s += 2) {
         step_body(s, std::integral_constant<int, 0>{});
         step_body(s + 1, std::integral_constant<int, 1>{});
     }
+    __syncthreads();  // everything landed before the epilogue reuses the LDS
 
-    // epilogue: passes of 32 rows through LDS; per (row, 128-block) one wave
-    // applies the output FWHT, norm and svh.  Accumulator (rb, G, c, r) is
-    // row 16rb + 4g + r, column 64cw + 32G + 16(i >> 3) + (i & 7) + 8c.
+    // epilogue: 4 passes through LDS, pass p holding tile rows 32p .. +32 of
+    // each half (LDS row rh*32 + local); the output FWHT, norm and svh per
+    // (row, 128-block).  Accumulator (rb, G, c, r) is tile row
+    // 128rh + 16rb + 4g + r, column 64cq + 32G + 16(i >> 3) + (i & 7) + 8c.
     float* ct = reinterpret_cast<float*>(fat_smem);
-    constexpr int PRB = FB_PASS_ROWS / 16;
 #pragma unroll
-    for (int pass = 0; pass < RB / PRB; ++pass) {
-        if (pass * FB_PASS_ROWS >= rows) break;
+    for (int pass = 0; pass < RB / 2; ++pass) {
+        if (pass * 32 >= rows) break;
         if (pass) __syncthreads();
 #pragma unroll
-        for (int rr = 0; rr < PRB; ++rr)
+        for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
             for (int G = 0; G < 2; ++G)
 #pragma unroll
                 for (int c = 0; c < 2; ++c)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int row = rr * 16 + 4 * g + r;
-                        const int col = cw * 64 + G * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                        ct[row * FB_CTS + col] = acc[pass * PRB + rr][G][c][r];
+                        const int row = rh * 32 + rr * 16 + 4 * g + r;
+                        const int col = cq * 64 + G * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                        ct[row * FB_CTS + col] = acc[pass * 2 + rr][G][c][r];
                     }
         __syncthreads();
-        const int prow = min(FB_PASS_ROWS, rows - pass * FB_PASS_ROWS);
-        for (int item = cw; item < prow * (FB_COLS / 128); item += FB_THREADS / 64) {
-            const int row = item / (FB_COLS / 128), b = item - row * (FB_COLS / 128);
-            const float2 v = *reinterpret_cast<const float2*>(ct + row * FB_CTS + b * 128 + 2 * lane);
-            float va = v.x, vb = v.y;
-            const int c0 = bx * FB_COLS + b * 128 + 2 * lane;
-            const __half2 sv = ld_h2(gptr(p.svh) + c0);
-            fwht128_pair_f(va, vb, lane);
-            va = (va * kHadNorm) * __low2float(sv);
-            vb = (vb * kHadNorm) * __high2float(sv);
-            const int src = m0 + pass * FB_PASS_ROWS + row;
-            if (p.out16) {
-                st_h2(gptr(p.out16) + (size_t)src * p.n + c0, __floats2half2_rn(va, vb));
+        // 8 rows x one 128-block per wave at a time: lane l holds 16 consecutive
+        // columns (16 (l & 7) ..) of LDS row 8 rg + (l >> 3)
+#pragma unroll
+        for (int gi = wv; gi < FB_PASS_ROWS / 8 * (FB_COLS / 128); gi += FB_THREADS / 64) {
+            const int b = gi & 1, rg = gi >> 1;
+            const int ctr = rg * 8 + (lane >> 3);
+            const int trow = (ctr >> 5) * 128 + pass * 32 + (ctr & 31);
+            const int col = b * 128 + (lane & 7) * 16;
+            float v[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 t = *reinterpret_cast<const float4*>(ct + ctr * FB_CTS + col + 4 * q);
+                v[4 * q] = t.x;
+                v[4 * q + 1] = t.y;
+                v[4 * q + 2] = t.z;
+                v[4 * q + 3] = t.w;
+            }
+            fwht128_x16(v, lane);
+            const int c0 = bx * FB_COLS + col;
+            // svh and the outputs are only 4- (8-) byte aligned by contract
+            const EXL3_GLOBAL uint32_t* svp = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh) + c0);
+            uint32_t sw[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sw[e] = svp[e];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const __half sv = __ushort_as_half((unsigned short)(sw[e >> 1] >> (16 * (e & 1))));
+                v[e] = (v[e] * kHadNorm) * __half2float(sv);
+            }
+            if (p.accumulate) {
+                // atomics want a wave's lanes on consecutive columns: the
+                // transformed rows go back to LDS (this wave's own rows) and
+                // leave as (row, 2 columns per lane) pairs
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<float4*>(ct + ctr * FB_CTS + col + 4 * q) =
+                        make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+#pragma unroll
+                for (int r8 = 0; r8 < 8; ++r8) {
+                    const int cr = rg * 8 + r8;
+                    const int tr = (cr >> 5) * 128 + pass * 32 + (cr & 31);
+                    if (tr >= rows) continue;
+                    const float2 pv = *reinterpret_cast<const float2*>(ct + cr * FB_CTS + b * 128 + 2 * lane);
+                    const int src = m0 + tr;
+                    size_t dst = (size_t)src;
+                    if (p.token_idx) dst = (size_t)gptr(p.token_idx)[src];
+                    float rw = 1.f;
+                    if (p.route_w)
+                        rw = __half2float(__ushort_as_half(gptr(reinterpret_cast<const uint16_t*>(p.route_w))[src]));
+                    float* o = p.out32 + dst * p.n + bx * FB_COLS + b * 128 + 2 * lane;
+                    atomicAdd(o, pv.x * rw);
+                    atomicAdd(o + 1, pv.y * rw);
+                }
                 continue;
             }
-            size_t dst = (size_t)src;
-            if (p.token_idx) dst = (size_t)gptr(p.token_idx)[src];
-            if (p.route_w) {
-                const float rw =
-                    __half2float(__ushort_as_half(gptr(reinterpret_cast<const uint16_t*>(p.route_w))[src]));
-                va *= rw;
-                vb *= rw;
+            if (trow >= rows) continue;
+            const int src = m0 + trow;
+            if (p.out16) {
+                __half* o = p.out16 + (size_t)src * p.n + c0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) st_h2(gptr(o) + 2 * e, __floats2half2_rn(v[2 * e], v[2 * e + 1]));
+                continue;
             }
-            float* o = p.out32 + dst * p.n + c0;
-            if (p.accumulate) {
-                atomicAdd(o, va);
-                atomicAdd(o + 1, vb);
-            } else {
-                const float2 v2 = make_float2(va, vb);
-                *reinterpret_cast<EXL3_GLOBAL unsigned long long*>(gptr(o)) =
+            float* o = p.out32 + (size_t)src * p.n + c0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float2 v2 = make_float2(v[2 * e], v[2 * e + 1]);
+                reinterpret_cast<EXL3_GLOBAL unsigned long long*>(gptr(o))[e] =
                     *reinterpret_cast<const unsigned long long*>(&v2);
             }
         }

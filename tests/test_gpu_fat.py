@@ -80,9 +80,9 @@ def _fat(a, tr, sv, K, cb, M, n):
 @pytest.mark.parametrize("K", range(1, 9))
 @pytest.mark.parametrize("cb", [0, 1, 2])
 def test_fat_wide_tiles_every_width(K, cb):
-    """Wide-tile kernel (128 x 256 tiles, from 65 rows): every bit width and codebook,
-    a partial second row tile, two k-splits accumulating atomically."""
-    M, k, n = 130, 256, 256
+    """Wide-tile kernel (256 x 256 tiles, from 65 rows): every bit width and codebook,
+    a partial second row tile (ending in the first row half), k-splits accumulating atomically."""
+    M, k, n = 300, 256, 256
     print(f"case: fat wide M={M} k={k} n={n} K={K} cb={cb}", flush=True)
     tr, su, sv = make_weight(k, n, K, seed=100 + 3 * K + cb)
     a = _rotate(make_x(M, k, seed=K + 10 * cb), su)
