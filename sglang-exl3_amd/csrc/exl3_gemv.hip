@@ -93,7 +93,10 @@ int env_int(const char* name, int dflt) {
 // (per-step work, per-workgroup overhead, and the latency that fewer than
 // four workgroups per CU leave exposed).  From m = 2 on the k-split kernel is
 // used: the balanced kernel's per-workgroup input rotation grows with m
-// (measured at m = 2, 4, 8).  Returns false when the balanced kernel does not
+// (measured at m = 2, 4, 8), and a variant fed by a separate row-rotation pass
+// was slower too at every piece count (config 2, m = 2 / 8: 14.7 / 23.4 us
+// against 13.7 / 20.1 us; the extra launch and the m x n x P fixed-point adds
+// outweigh the balance).  Returns false when the balanced kernel does not
 // apply.
 bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {
     if (experts != 1 || m != 1 || env_int("EXL3_GEMV_SK", 1) == 0) return false;
