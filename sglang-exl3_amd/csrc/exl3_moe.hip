@@ -253,20 +253,21 @@ double expected_active(int tokens, int topk, int E) {
 
 // Launch shape of one expert projection pass, by a rule fitted to graph-timed
 // sweeps on MI355X (config 4 at B = 1/16/64 and config 5):
-//  * few units (< 16): 2 k-waves x 4 steps per workgroup and more k-splits
-//    (latency-bound, parallelism matters);
-//  * otherwise 1 k-wave x 8 steps (4 where 32 k-slices do not divide k);
-//  * column blocks per item grouped only when the items would exceed about
-//    eight times the persistent grid (two 8-wave workgroups per CU).
+//  * 1 k-wave x 8 steps per workgroup (4 where 32 k-slices do not divide k).
+//    With one k-wave the partial rows leave straight from the accumulators, so
+//    four workgroups fit a CU; that beat 2 k-waves x 4 steps at every batch
+//    (config 4, B = 1 / 16 / 64: 26.2 / 60.1 / 113.9 us against
+//    27.0 / 67.5 / 136.7 us);
+//  * column blocks per item grouped only when the items would exceed
+//    8 x 512 (a few per workgroup of the persistent grid).
 // Env overrides (tuning): EXL3_MOE_NSTEPS, EXL3_MOE_KW, EXL3_MOE_BPI.
 MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
     (void)entries;
     const int kslices = k / 16, nblk = n / 128;
     const double grid = 512.0;
-    const bool few = units < 16.0;
-    int kw = env_int("EXL3_MOE_KW", few ? 2 : 1);
+    int kw = env_int("EXL3_MOE_KW", 1);
     if (kw != 1 && kw != 2) kw = 1;
-    int ns = env_int("EXL3_MOE_NSTEPS", few ? 4 : 8);
+    int ns = env_int("EXL3_MOE_NSTEPS", 8);
     while (ns > 2 && (kslices % (4 * ns * kw) || (4 * ns * kw) % 8 ||
                       moe_smem_bytes(4 * ns * kw, kw) > kMaxLds / 2 - 1024))
         ns /= 2;

@@ -107,7 +107,7 @@ __device__ __forceinline__ __half2 ld_h2_ptr(const void* base, int idx) {
 // arrives rotated), decode + MFMA the split's k range for 128 columns, store
 // fp32 partial rows; the last of nproj * S arrivals of (unit, column block)
 // runs the epilogue.
-template <int K, int CB, int NS, int MODE>
+template <int K, int CB, int NS, int MODE, int KW>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
     constexpr int ROWS = MOE_UNIT_ROWS;
     extern __shared__ __align__(16) unsigned char mv_smem[];
@@ -121,7 +121,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     const int total = nunits * per_unit;
     if ((int)blockIdx.x >= total) return;
 
-    const int k = p.k, n = p.n, kw = p.kw;
+    const int k = p.k, n = p.n;
+    constexpr int kw = KW;  // k waves (p.kw)
     constexpr int nsteps = NS;
     const int nthreads = 256 * kw, nwaves = 4 * kw;
     const int kts_wg = 4 * nsteps * kw;
@@ -253,27 +254,48 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
             decode_mfma_steps<K, CB, 1, NS>(w, tiles(bx), step_stride, a_base, a_live, acc);
 
             // 4. k waves summed through LDS, mul1 affine map, partial rows out
-#pragma unroll
-            for (int c = 0; c < 2; ++c)
+            //    (one k wave: straight from the accumulators, no LDS tile, so
+            //    four workgroups fit a CU)
+            float* part =
+                p.partials + ((size_t)(bx * p.nproj + proj) * S + sidx) * split_stride + (size_t)crow0 * 128;
+            if constexpr (KW == 1) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 4 * g + r;
-                    const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                    if (row < m) ybuf[(kwi * ROWS + row) * 128 + col] = acc[0][c][r];
-                }
-            __syncthreads();
-            float* part =
-                p.partials + ((size_t)(bx * p.nproj + proj) * S + sidx) * split_stride + (size_t)crow0 * 128;
-            for (int idx = tid; idx < m * 128; idx += nthreads) {
-                float v = ybuf[idx];
-                for (int j = 1; j < kw; ++j) v += ybuf[j * ROWS * 128 + idx];
-                if constexpr (CB == 2) {
-                    const int row = idx >> 7;
+                    if (row >= m) continue;
                     float sx = 0.f;
-                    for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
-                    v = v * kMul1Kinv + kMul1Delta * sx;
+                    if constexpr (CB == 2)
+                        for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                        float v = acc[0][c][r];
+                        if constexpr (CB == 2) v = v * kMul1Kinv + kMul1Delta * sx;
+                        coherent_store(part + row * 128 + col, v);
+                    }
                 }
-                coherent_store(part + idx, v);
+            }
+            else {
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = 4 * g + r;
+                        const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                        if (row < m) ybuf[(kwi * ROWS + row) * 128 + col] = acc[0][c][r];
+                    }
+                __syncthreads();
+                for (int idx = tid; idx < m * 128; idx += nthreads) {
+                    float v = ybuf[idx];
+                    for (int j = 1; j < kw; ++j) v += ybuf[j * ROWS * 128 + idx];
+                    if constexpr (CB == 2) {
+                        const int row = idx >> 7;
+                        float sx = 0.f;
+                        for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+                        v = v * kMul1Kinv + kMul1Delta * sx;
+                    }
+                    coherent_store(part + idx, v);
+                }
             }
 
             // 5. hand-off: the last of nproj * S arrivals for (unit, column
@@ -363,7 +385,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
 inline size_t moe_smem_bytes(int kts_wg, int kw) {
     const int rows = MOE_UNIT_ROWS;
     const size_t xs = ((size_t)kts_wg * 4 * rows * 8 * 2 + 16 + 15) & ~(size_t)15;
-    return xs + (size_t)((rows * (kts_wg / 8) + 3) & ~3) * 4 + (size_t)kw * rows * 128 * 4;
+    return xs + (size_t)((rows * (kts_wg / 8) + 3) & ~3) * 4 + (kw > 1 ? (size_t)kw * rows * 128 * 4 : 0);
 }
 
 // Workgroups of moe_gemv_kernel<...> the device holds at once (cached).
@@ -374,16 +396,17 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     const size_t smem = moe_smem_bytes(4 * ns * p.kw, p.kw);
     const int threads = 256 * p.kw;
     const int mv = p.mode == MOE_DOWN ? MV_DOWN : (p.in_rot ? MV_GU_ROT : MV_GU);
-#define EXL3_MV_NS(CBV, NSV, MVV)                                                                      \
-    if (cb == CBV && ns == NSV && mv == MVV) {                                                         \
-        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV>);            \
+#define EXL3_MV_KW(CBV, NSV, MVV, KWV)                                                                 \
+    if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV) {                                          \
+        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV>);       \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe");                                       \
         if (lrc) return lrc;                                                                           \
         const int grid = moe_grid_size(fn, threads, smem);                                             \
         if (grid <= 0) return EXL3_ERR_HIP;                                                            \
-        moe_gemv_kernel<K, CBV, NSV, MVV><<<grid, threads, smem, st>>>(p);                             \
+        moe_gemv_kernel<K, CBV, NSV, MVV, KWV><<<grid, threads, smem, st>>>(p);                        \
         return launch_status("exl3 moe launch");                                                      \
     }
+#define EXL3_MV_NS(CBV, NSV, MVV) EXL3_MV_KW(CBV, NSV, MVV, 1) EXL3_MV_KW(CBV, NSV, MVV, 2)
 #define EXL3_MV_MODES(CBV, NSV) EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)
 #define EXL3_MV_CASE(CBV) \
     EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 16)
@@ -391,7 +414,8 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
 #undef EXL3_MV_CASE
 #undef EXL3_MV_MODES
 #undef EXL3_MV_NS
-    set_error("exl3 moe: no kernel for codebook %d steps %d", cb, ns);
+#undef EXL3_MV_KW
+    set_error("exl3 moe: no kernel for codebook %d steps %d k waves %d", cb, ns, p.kw);
     return EXL3_ERR_UNSUPPORTED;
 }
 
