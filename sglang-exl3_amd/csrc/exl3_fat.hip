@@ -62,9 +62,9 @@ struct FatPlan {
 };
 
 // Wide tiles (256 x 256, fat_big_kernel) from kFatWideRows rows on (env
-// EXL3_FAT_WIDE=0 turns them off); below, rows per tile from M.  k-splits until
-// the grid fills the chip: ~4 workgroups per CU for the narrow kernel (each
-// split a whole number of FAT_CH chunks).  The wide kernel splits only grids
+// EXL3_FAT_WIDE=0 turns them off); below, rows per tile from M.  k-splits for
+// the narrow kernel toward ~4 workgroups per CU (each split a whole number of
+// FAT_CH chunks), capped by the atomics they add.  The wide kernel splits only grids
 // under 96 workgroups (an even number of steps per split): its outputs are
 // large, and split outputs cost a zero fill plus one fp32 atomic per value
 // and split, which measured slower than leaving up to 60 % of the CUs idle.
@@ -84,8 +84,14 @@ FatPlan plan_fat(int M, int k, int n) {
     }
     pl.mt = M >= 128 ? 128 : (M > 16 ? 64 : 16);
     const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
-    while (base * pl.splits < 1024 && pl.splits < 16 && ksteps % (2 * pl.splits) == 0 &&
-           (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+    const char* fs = getenv("EXL3_FAT_SPLITS");  // tuning override (power of two)
+    const int forced = fs ? atoi(fs) : 0;
+    // every split adds M x n fp32 atomics: stop doubling before they pass 2^21
+    // (n = 28672: M = 16 takes 4 splits, M = 32 two, M = 64 one; 1.1-1.9x
+    // faster than filling the chip with splits)
+    while ((forced ? pl.splits < forced
+                   : base * pl.splits < 1024 && (long long)M * n * 2 * pl.splits <= (1LL << 21)) &&
+           pl.splits < 16 && ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
         pl.splits *= 2;
     return pl;
 }
