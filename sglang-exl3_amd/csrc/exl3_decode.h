@@ -103,6 +103,82 @@ __device__ __forceinline__ void fwht128_pair_f(float& a, float& b, int lane) {
     fwht_stage<32>(a, b, lane);
 }
 
+// fp16 round-to-nearest of a value already rounded to fp32.  Without the empty
+// asm the backend folds the multiply (or fma) that produced v into
+// v_fma_mixlo/hi_f16, which rounds the exact result to fp16 once: on MI355X
+// that gave another fp16 for ~6e-5 of products, where the reference rounds
+// the fp32 product (fp32 multiply, then __float2half_rn).
+__device__ __forceinline__ _Float16 f16_rn(float v) {
+    asm("" : "+v"(v));
+    return (_Float16)v;
+}
+__device__ __forceinline__ __half2 h2_rn(float a, float b) {
+    asm("" : "+v"(a), "+v"(b));
+    return __floats2half2_rn(a, b);
+}
+
+// +1.0f where bit J of lane is clear, -1.0f where it is set.
+template <int J>
+__device__ __forceinline__ float lane_sign(int lane) {
+    return __uint_as_float(0x3f800000u | ((uint32_t)(lane & J) << (31 - __builtin_ctz(J))));
+}
+
+// The same transform as fwht128_pair_f in about 20 VALU instead of ~50, with
+// the same rounded magnitudes; a result that is exactly zero may differ in
+// sign (fwht128_pair_f stays the path of the bit-exact operators).
+//   * Stages of stride 2..16 (lane bits 0..3) run on values that carry the
+//     sign s = (-1)^popcount(lane & done bits): each is one fma with the
+//     partner's value as its DPP operand, h' = h + c p with c = -1 on the
+//     upper lane, so h' = s (x + y) below and h' = -s (y - x) above (one
+//     rounding of the same sum).  The partner always carries the same s.
+//   * Strides 32 and 64 (lane bits 4, 5): a permlane16 / permlane32 swap of
+//     (a, b) gives each lane both operands of a butterfly, which then runs in
+//     registers; two more swaps restore value 2 lane in a and 2 lane + 1 in b.
+//   * The final s is multiplied out (exact).
+__device__ __forceinline__ void fwht128_pair_fast(float& a, float& b, int lane) {
+    float x = a + b, y = a - b;
+    const float c1 = lane_sign<1>(lane), c2 = lane_sign<2>(lane), c4 = lane_sign<4>(lane), c8 = lane_sign<8>(lane);
+    float t, u;
+    // The compiler does not fold a DPP move into v_fmac, so the four stages are
+    // written out.  A VGPR written by a VALU op needs two wait states before a
+    // DPP read of it: the s_nop count plus the VALU ops in between give them.
+    asm(
+        "s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %0, %4 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %1, %4 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 0\n\t"
+        "v_fmac_f32_dpp %0, %0, %5 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %1, %5 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 0\n\t"
+        // lane ^ 4 = (lane ^ 7) ^ 3: row_half_mirror, then quad_perm [3,2,1,0]
+        "v_mov_b32_dpp %2, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b32_dpp %3, %1 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 0\n\t"
+        "v_fmac_f32_dpp %0, %2, %6 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %3, %6 quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 0\n\t"
+        "v_fmac_f32_dpp %0, %0, %7 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %1, %1, %7 row_ror:8 row_mask:0xf bank_mask:0xf"
+        : "+v"(x), "+v"(y), "=&v"(t), "=&v"(u)
+        : "v"(c1), "v"(c2), "v"(c4), "v"(c8));
+    // rows (r0, r1, r2, r3): a' = (x.r0, y.r0, x.r2, y.r2), b' = (x.r1, y.r1, x.r3, y.r3)
+    auto w = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    float p = __uint_as_float(w[0]), q = __uint_as_float(w[1]);
+    x = p + q;
+    y = p - q;
+    // halves: a' = (x.lo, y.lo), b' = (x.hi, y.hi)
+    w = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    p = __uint_as_float(w[0]);
+    q = __uint_as_float(w[1]);
+    x = p + q;
+    y = p - q;
+    w = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    w = __builtin_amdgcn_permlane16_swap(w[0], w[1], false, false);
+    const float s = __uint_as_float(0x3f800000u | ((uint32_t)__builtin_popcount(lane & 15) << 31));
+    a = __uint_as_float(w[0]) * s;
+    b = __uint_as_float(w[1]) * s;
+}
+
 // The same transform with one row held as 16 consecutive values per lane over
 // 8 lanes (value 16 (lane & 7) + e in v[e]): stages of stride 1 .. 8 in
 // registers, 16 .. 64 across the lanes (xor 1, 2, 4), in the same order and

@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void rotate_rows_kernel(const __half* x, const
     const int c = (int)(chunk - row * per_row) * 128 + 2 * lane;
     const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)row * k + c), ld_h2(gptr(suh) + c));
     float a = __low2float(pr), b = __high2float(pr);
-    fwht128_pair_f(a, b, lane);
-    st_h2(gptr(xr) + (size_t)row * k + c, __floats2half2_rn(a * kHadNorm, b * kHadNorm));
+    fwht128_pair_fast(a, b, lane);
+    st_h2(gptr(xr) + (size_t)row * k + c, h2_rn(a * kHadNorm, b * kHadNorm));
 }
 
 struct FatPlan {

@@ -153,12 +153,12 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
     const int c0 = bx * 128 + 2 * lane;
     for (int row = cw; row < rows; row += FAT_THREADS / 64) {
         float va = ct[row * 128 + 2 * lane], vb = ct[row * 128 + 2 * lane + 1];
-        fwht128_pair_f(va, vb, lane);
+        fwht128_pair_fast(va, vb, lane);
         va = (va * kHadNorm) * sva;
         vb = (vb * kHadNorm) * svb;
         const int src = m0 + row;
         if (p.out16) {
-            st_h2(gptr(p.out16) + (size_t)src * p.n + c0, __floats2half2_rn(va, vb));
+            st_h2(gptr(p.out16) + (size_t)src * p.n + c0, h2_rn(va, vb));
             continue;
         }
         size_t dst = (size_t)src;
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
             if (p.out16) {
                 __half* o = p.out16 + (size_t)src * p.n + c0;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) st_h2(gptr(o) + 2 * e, __floats2half2_rn(v[2 * e], v[2 * e + 1]));
+                for (int e = 0; e < 8; ++e) st_h2(gptr(o) + 2 * e, h2_rn(v[2 * e], v[2 * e + 1]));
                 continue;
             }
             float* o = p.out32 + (size_t)src * p.n + c0;

@@ -317,8 +317,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         const int kk = bb * 128 + 2 * lane;
         const __half2 pr = __hmul2(xv, sv);
         float a = __low2float(pr), c = __high2float(pr);
-        fwht128_pair_f(a, c, lane);
-        const _Float16 ha = (_Float16)(a * kHadNorm), hc = (_Float16)(c * kHadNorm);
+        fwht128_pair_fast(a, c, lane);
+        const _Float16 ha = f16_rn(a * kHadNorm), hc = f16_rn(c * kHadNorm);
         const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
         xs[ia] = ha;
         xs[ia + 1] = ha;
@@ -414,8 +414,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     const float sva = __low2float(svv), svb = __high2float(svv);
     for (int row = wave; row < m; row += nwaves) {
         float a = ybuf[row * 128 + 2 * lane], b = ybuf[row * 128 + 2 * lane + 1];
-        fwht128_pair_f(a, b, lane);
-        const __half2 o = __floats2half2_rn(a * kHadNorm * sva, b * kHadNorm * svb);
+        fwht128_pair_fast(a, b, lane);
+        const __half2 o = h2_rn(a * kHadNorm * sva, b * kHadNorm * svb);
         st_h2(y + (size_t)row * n + c0, o);
     }
 }

@@ -119,8 +119,8 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
         const __half2 sv = jb == cw ? s0 : ld_h2(suhg + j * 128);
         const __half2 pr = __hmul2(xv, sv);
         float a = __low2float(pr), c = __high2float(pr);
-        fwht128_pair_f(a, c, lane);
-        const _Float16 ha = (_Float16)(a * kHadNorm), hc = (_Float16)(c * kHadNorm);
+        fwht128_pair_fast(a, c, lane);
+        const _Float16 ha = f16_rn(a * kHadNorm), hc = f16_rn(c * kHadNorm);
         if (mine) {
             // (ha, ha, hc, hc): the two values, each duplicated, in one 8-byte store
             const uint32_t da = (uint32_t)__builtin_bit_cast(unsigned short, ha) * 0x10001u;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
         a = a * kMul1Kinv + kMul1Delta * sx;
         b = b * kMul1Kinv + kMul1Delta * sx;
     }
-    fwht128_pair_f(a, b, lane);
+    fwht128_pair_fast(a, b, lane);
     a = a * kHadNorm * __low2float(svv);
     b = b * kHadNorm * __high2float(svv);
     const int e0 = cb * 128 + 2 * lane;

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(HAD_THREADS) void hadamard_rows_kernel(const __half
         a *= s.x;
         b *= s.y;
     }
-    const __half2 o = __floats2half2_rn(a, b);
+    const __half2 o = h2_rn(a, b);
     *reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(y) + off) = *reinterpret_cast<const uint32_t*>(&o);
 }
 

@@ -142,8 +142,8 @@ __global__ __launch_bounds__(256) void moe_rotate_kernel(const __half* x, const 
     const int kg = j * 128 + 2 * lane;
     const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)(entry / topk) * hidden + kg), ld_h2(gptr(suh) + kg));
     float a = __low2float(pr), c = __high2float(pr);
-    fwht128_pair_f(a, c, lane);
-    st_h2(gptr(xr) + ((size_t)proj * entries + crow) * hidden + kg, __floats2half2_rn(a * kHadNorm, c * kHadNorm));
+    fwht128_pair_fast(a, c, lane);
+    st_h2(gptr(xr) + ((size_t)proj * entries + crow) * hidden + kg, h2_rn(a * kHadNorm, c * kHadNorm));
 }
 
 // ------------------------------------------------------------------ combine
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const __half* y, const
         a0 += wv * __low2float(v);
         a1 += wv * __high2float(v);
     }
-    st_h2(gptr(out) + (size_t)t * hidden + c, __floats2half2_rn(a0, a1));
+    st_h2(gptr(out) + (size_t)t * hidden + c, h2_rn(a0, a1));
 }
 
 static int env_int_once(const char* name) {

@@ -202,9 +202,9 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
             } else {
                 const __half2 pr = __hmul2(xv, sv);
                 float fa = __low2float(pr), fc = __high2float(pr);
-                fwht128_pair_f(fa, fc, lane);
-                ha = (_Float16)(fa * kHadNorm);
-                hc = (_Float16)(fc * kHadNorm);
+                fwht128_pair_fast(fa, fc, lane);
+                ha = f16_rn(fa * kHadNorm);
+                hc = f16_rn(fc * kHadNorm);
             }
             const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
             xs[ia] = ha;
@@ -344,13 +344,13 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                     float2 gu[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
                     sum_rows(2, crow, gu);
                     float ga = gu[0].x, gb = gu[0].y, ua = gu[1].x, ub = gu[1].y;
-                    fwht128_pair_f(ga, gb, lane);
-                    fwht128_pair_f(ua, ub, lane);
+                    fwht128_pair_fast(ga, gb, lane);
+                    fwht128_pair_fast(ua, ub, lane);
                     // gate and up outputs in fp16, as the separate linears return them
                     const __half2 gh =
-                        __floats2half2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
+                        h2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
                     const __half2 uh =
-                        __floats2half2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
+                        h2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
                     float g0 = __low2float(gh), g1 = __high2float(gh), u0 = __low2float(uh), u1 = __high2float(uh);
                     if (clamp) {
                         g0 = fminf(g0, p.limit);
@@ -358,12 +358,12 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                         u0 = fminf(fmaxf(u0, -p.limit), p.limit);
                         u1 = fminf(fmaxf(u1, -p.limit), p.limit);
                     }
-                    const __half2 act = __floats2half2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
+                    const __half2 act = h2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
                     // input rotation of the down projection for this 128-wide chunk
                     const __half2 pr = __hmul2(act, ev2);
                     float da = __low2float(pr), db = __high2float(pr);
-                    fwht128_pair_f(da, db, lane);
-                    st_h2(outg + (size_t)crow * n + c0, __floats2half2_rn(da * kHadNorm, db * kHadNorm));
+                    fwht128_pair_fast(da, db, lane);
+                    st_h2(outg + (size_t)crow * n + c0, h2_rn(da * kHadNorm, db * kHadNorm));
                 }
             } else {
                 for (int row = wave; row < m; row += nwaves) {
@@ -371,10 +371,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                     float2 d[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
                     sum_rows(1, crow, d);
                     float va = d[0].x, vb = d[0].y;
-                    fwht128_pair_f(va, vb, lane);
+                    fwht128_pair_fast(va, vb, lane);
                     const int entry = rows_g[crow];
                     st_h2(outg + (size_t)entry * n + c0,
-                          __floats2half2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0)));
+                          h2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0)));
                 }
             }
         }
