@@ -132,21 +132,41 @@ __device__ __forceinline__ float sk_decode(unsigned long long total, int cnt) {
     return (float)v * (1.0f / SK_FX_SCALE);
 }
 
-// Add a and b to the accumulators acc[0] and acc[1] (device scope); the add
-// that brings an element to `cnt` contributions stores it to y (fp16) and
-// clears the accumulator for the next call.
-__device__ __forceinline__ void fx_add_pair(unsigned long long* acc, float a, float b, int cnt, EXL3_GLOBAL __half* y) {
-    const unsigned long long ea = sk_encode(a), eb = sk_encode(b);
-    const unsigned long long oa = __hip_atomic_fetch_add(acc, ea, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long ob = __hip_atomic_fetch_add(acc + 1, eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((int)(oa >> SK_CNT_SHIFT) == cnt - 1) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y) = __half_as_ushort(__float2half_rn(sk_decode(oa + ea, cnt)));
+// Two adjacent contributions in flight: the encoded addends and the values
+// the atomic adds returned.
+struct FxPair {
+    unsigned long long ea, eb, oa, ob;
+};
+
+// Add a and b to the accumulators acc[0] and acc[1] (device scope).  The
+// returned values are only read by fx_finish_pair, so several pairs can be
+// in flight before the first wait.
+__device__ __forceinline__ FxPair fx_issue_pair(unsigned long long* acc, float a, float b) {
+    FxPair f;
+    f.ea = sk_encode(a);
+    f.eb = sk_encode(b);
+    f.oa = __hip_atomic_fetch_add(acc, f.ea, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f.ob = __hip_atomic_fetch_add(acc + 1, f.eb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return f;
+}
+
+// The add that brought an element to `cnt` contributions stores it to y
+// (fp16) and clears the accumulator for the next call.
+__device__ __forceinline__ void fx_finish_pair(const FxPair& f, unsigned long long* acc, int cnt,
+                                               EXL3_GLOBAL __half* y) {
+    if ((int)(f.oa >> SK_CNT_SHIFT) == cnt - 1) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y) = __half_as_ushort(__float2half_rn(sk_decode(f.oa + f.ea, cnt)));
         __hip_atomic_store(acc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if ((int)(ob >> SK_CNT_SHIFT) == cnt - 1) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + 1) = __half_as_ushort(__float2half_rn(sk_decode(ob + eb, cnt)));
+    if ((int)(f.ob >> SK_CNT_SHIFT) == cnt - 1) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + 1) =
+            __half_as_ushort(__float2half_rn(sk_decode(f.ob + f.eb, cnt)));
         __hip_atomic_store(acc + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+__device__ __forceinline__ void fx_add_pair(unsigned long long* acc, float a, float b, int cnt, EXL3_GLOBAL __half* y) {
+    fx_finish_pair(fx_issue_pair(acc, a, b), acc, cnt, y);
 }
 
 // Wait until this wave's outstanding memory operations have completed.

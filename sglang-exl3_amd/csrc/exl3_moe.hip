@@ -43,23 +43,45 @@ struct MoeTables {
 // up to 16 rows, with the expert's nine weight addresses resolved.  Entries
 // with ids outside [0, E) are dropped.  Row order inside an expert follows
 // LDS atomics; each row's product is independent of its position, so results
-// do not depend on it.
+// do not depend on it.  Also counts each token's valid slots (the fused
+// combine's completion count) and, when the combine is fused, writes the zero
+// output row of a token without any valid slot.
 __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int32_t* ids, int entries, int E,
-                                                                     MoeTables tabs, MoeRoute rt) {
+                                                                     MoeTables tabs, MoeRoute rt, int topk,
+                                                                     int* tok_valid, __half* out, int hidden,
+                                                                     int fc) {
     extern __shared__ __align__(16) int rt_smem[];
     int* cnt = rt_smem;    // [E]
     int* off = cnt + E;    // [E] first compact row
     int* uoff = off + E;   // [E] first unit
     int* pos = uoff + E;   // [entries]
-    const int tid = threadIdx.x;
+    int* tv = pos + entries;  // [tokens] valid slots
+    __shared__ int any_empty;
+    const int tid = threadIdx.x, tokens = entries / topk;
     for (int e = tid; e < E; e += MOE_ROUTE_THREADS) cnt[e] = 0;
+    for (int t = tid; t < tokens; t += MOE_ROUTE_THREADS) tv[t] = 0;
+    if (tid == 0) any_empty = 0;
     __syncthreads();
     const EXL3_GLOBAL int32_t* idg = gptr(ids);
     for (int i = tid; i < entries; i += MOE_ROUTE_THREADS) {
         const int e = idg[i];
-        pos[i] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
+        const bool valid = e >= 0 && e < E;
+        pos[i] = valid ? atomicAdd(&cnt[e], 1) : -1;
+        if (valid) atomicAdd(&tv[i / topk], 1);
     }
     __syncthreads();
+    for (int t = tid; t < tokens; t += MOE_ROUTE_THREADS) {
+        gptr(tok_valid)[t] = tv[t];
+        if (tv[t] == 0) any_empty = 1;
+    }
+    __syncthreads();
+    if (fc && any_empty) {
+        const int hp = hidden >> 1;  // fp16 pairs per row
+        for (int idx = tid; idx < tokens * hp; idx += MOE_ROUTE_THREADS) {
+            const int t = idx / hp;
+            if (tv[t] == 0) reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(out) + (size_t)t * hidden)[idx - t * hp] = 0u;
+        }
+    }
     // exclusive scans over the experts (rows, units, active), one wave
     if (tid < 64) {
         const int chunk = (E + 63) / 64;
@@ -293,12 +315,13 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
 // pass of their own (moe_rotate_kernel); below it each GEMV item rotates its
 // rows (one row per unit at one token: nothing to share).
 constexpr int kMoeRotTokens = 8;
+constexpr int kMoeFusedCombineTokens = 16;
 
 struct MoeLayout {
     int entries, max_units;
-    bool rot;
+    bool rot, fc;
     MoePlan gu, dn;
-    size_t route_off, units_off, rows_off, h_off, y_off, xr_off, part_off, total;
+    size_t route_off, units_off, rows_off, tokv_off, h_off, y_off, xr_off, part_off, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -320,6 +343,18 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     o = align256(o + (size_t)L.max_units * sizeof(MoeUnit));
     L.rows_off = o;
     o = align256(o + (size_t)L.entries * sizeof(int));
+    L.tokv_off = o;
+    o = align256(o + (size_t)tokens * sizeof(int));
+    // Up to kMoeFusedCombineTokens tokens the weighted combine runs inside the
+    // down pass (fixed-point output accumulators, 8 bytes per output, in the
+    // workspace's accumulator region).  Graph-timed on config 4 it saves the
+    // combine launch (B = 1 / 2 / 4 / 8 / 16: 27.8 / 32.6 / 36.1 / 49.9 / 64.5 us
+    // -> 24.6 / 29.3 / 32.8 / 47.4 / 63.6 us); from 32 tokens the contended
+    // 64-bit atomics (eight slots per output) cost more than the launch
+    // (B = 32 / 48 / 64: 100.2 / 114.3 / 117.0 -> 105.6 / 120.1 / 123.6 us).
+    // Env EXL3_MOE_FC_TOKENS overrides the threshold (0: never fused).
+    const int fc_tokens = env_int("EXL3_MOE_FC_TOKENS", kMoeFusedCombineTokens);
+    L.fc = tokens <= fc_tokens && (size_t)tokens * hidden * 8 <= kWsAccBytes && topk <= SK_MAX_CONTRIB;
     L.h_off = o;
     o = align256(o + (size_t)L.entries * inter * 2);
     L.y_off = o;
@@ -366,13 +401,15 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     rt.rows = reinterpret_cast<int*>(w8 + L.rows_off);
     __half* h = reinterpret_cast<__half*>(w8 + L.h_off);
     __half* yslots = reinterpret_cast<__half*>(w8 + L.y_off);
+    int* tok_valid = reinterpret_cast<int*>(w8 + L.tokv_off);
 
     // 1. routing
     {
-        const size_t smem = moe_route_smem_bytes(E, L.entries);
+        const size_t smem = moe_route_smem_bytes(E, L.entries, tokens);
         int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&moe_route_kernel), smem, "exl3 moe route");
         if (rc) return rc;
-        moe_route_kernel<<<1, MOE_ROUTE_THREADS, smem, st>>>(ids, L.entries, E, tb, rt);
+        moe_route_kernel<<<1, MOE_ROUTE_THREADS, smem, st>>>(ids, L.entries, E, tb, rt, topk, tok_valid,
+                                                             reinterpret_cast<__half*>(out), hidden, L.fc);
         rc = launch_status("exl3 moe route launch");
         if (rc) return rc;
     }
@@ -436,8 +473,15 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     p.splits = L.dn.splits;
     p.kw = L.dn.kw;
     p.bx_per_item = L.dn.bpi;
+    p.fc = L.fc;
+    p.acc = reinterpret_cast<unsigned long long*>(w8 + kWsAccOffset);
+    p.tok_valid = tok_valid;
+    p.weights = weights;
+    p.weights_f16 = weights_f16;
+    p.final_out = reinterpret_cast<__half*>(out);
     rc = moe_launch(KD, cb, L.dn.ns, p, st);
     if (rc) return rc;
+    if (L.fc) return EXL3_OK;
 
     // 5. weighted combine
     moe_combine_kernel<<<dim3((hidden / 2 + 255) / 256, tokens), 256, 0, st>>>(

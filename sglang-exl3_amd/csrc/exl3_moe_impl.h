@@ -12,7 +12,10 @@
 //            128-wide chunk, and stores the rotated activation row
 //   down     grid (hidden/128, S, slots): same product on the rotated
 //            activations; the last arrival applies the output rotation and
-//            stores each row at its (token, slot) entry
+//            adds w * y of each row into its token's fixed-point output
+//            accumulators, the add completing a token writing its fp16 row
+//            (deterministic: integer sums); without room for the
+//            accumulators it stores each row at its (token, slot) entry and
 //   combine  out[t] = sum over slots of w[t,slot] * y[t,slot] in fp32, in slot
 //            order (deterministic)
 //
@@ -79,9 +82,22 @@ struct MoeParams {
     int mode;
     int in_rot;        // GATE_UP: x holds the rows already rotated per projection,
                        // [2][entries][k] by compact row (moe_rotate_kernel)
+    // DOWN with the weighted combine fused (fc != 0): each row's w[entry] * y
+    // is added into 64-bit fixed-point accumulators acc[token][n]; the add that
+    // completes the token's valid-slot count writes the fp16 output and clears
+    // the accumulator (integer addition: the result does not depend on the
+    // order of arrival)
+    int fc;
+    unsigned long long* acc;  // [tokens][n], zero between calls
+    const int* tok_valid;     // [tokens] valid slots per token (routing kernel)
+    const void* weights;      // [entries] routing weights, fp16 or fp32
+    int weights_f16;
+    __half* final_out;        // [tokens][n]
 };
 
-inline size_t moe_route_smem_bytes(int E, int entries) { return (size_t)(3 * E + entries) * sizeof(int); }
+inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
+    return (size_t)(3 * E + entries + tokens) * sizeof(int);
+}
 
 // ------------------------------------------------------------ expert GEMVs
 
@@ -366,16 +382,42 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                     st_h2(outg + (size_t)crow * n + c0, h2_rn(da * kHadNorm, db * kHadNorm));
                 }
             } else {
+                // fused combine: a row's fixed-point adds are checked only
+                // after the next row's partials have been loaded, so their
+                // round trips overlap
+                FxPair fx{};
+                int ptok = -1, pcnt = 0;
                 for (int row = wave; row < m; row += nwaves) {
                     const int crow = crow0 + row;
                     float2 d[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
                     sum_rows(1, crow, d);
                     float va = d[0].x, vb = d[0].y;
                     fwht128_pair_fast(va, vb, lane);
-                    const int entry = rows_g[crow];
-                    st_h2(outg + (size_t)entry * n + c0,
-                          h2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0)));
+                    const int entry = uniform_i(rows_g[crow]);
+                    // the expert's output row in fp16, as the separate linear returns it
+                    const __half2 yh = h2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0));
+                    if (p.fc) {
+                        const int t = entry / p.topk;
+                        const float wv =
+                            p.weights_f16
+                                ? __half2float(__ushort_as_half(
+                                      gptr(reinterpret_cast<const uint16_t*>(p.weights))[entry]))
+                                : gptr(reinterpret_cast<const float*>(p.weights))[entry];
+                        const int c = uniform_i(gptr(p.tok_valid)[t]);
+                        const FxPair cur =
+                            fx_issue_pair(p.acc + (size_t)t * n + c0, wv * __low2float(yh), wv * __high2float(yh));
+                        if (ptok >= 0)
+                            fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt,
+                                           gptr(p.final_out) + (size_t)ptok * n + c0);
+                        fx = cur;
+                        ptok = t;
+                        pcnt = c;
+                    } else {
+                        st_h2(outg + (size_t)entry * n + c0, yh);
+                    }
                 }
+                if (ptok >= 0)
+                    fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
             }
         }
     }

@@ -231,6 +231,26 @@ def test_moe_rotation_pass(T, topk, E, cb, invalid, rot_tokens, monkeypatch):
     check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), f"moe rotation pass T={T}")
 
 
+@pytest.mark.parametrize("T,topk,E,fc_tokens", [(6, 4, 8, 0), (6, 4, 8, 16), (33, 2, 4, 100), (20, 8, 16, 100)])
+def test_moe_fused_combine(T, topk, E, fc_tokens, monkeypatch):
+    """Weighted combine in the down pass (fixed-point accumulators, fc_tokens >= T) or in its own
+    kernel (fc_tokens < T): both against the oracle, a token without valid slots gives a zero row,
+    and repeated calls give the same bits (the accumulators are left zero)."""
+    print(f"case: moe fused combine T={T} topk={topk} E={E} fc_tokens={fc_tokens}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_FC_TOKENS", str(fc_tokens))
+    ex = Experts(E, 256, 256, (3, 3, 3), 1, seed=90 + T)
+    x = make_x(T, 256, seed=91 + T)
+    ids, w = _routing(T, topk, E, seed=92 + T, invalid=3)
+    ids[T // 2, :] = -1
+    a = _layer_capi(ex, x, ids, w, cb=1)
+    b = _layer_capi(ex, x, ids, w, cb=1)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    o = a.float().cpu().numpy()
+    assert np.all(o[T // 2] == 0.0)
+    check_close(o, ex.ref(x, ids, w), f"moe fused combine T={T}")
+
+
 def test_moe_rejects_bad_arguments():
     ex = Experts(2, 256, 128, (2, 2, 2), 1, seed=1)
     x = torch.zeros((1, 200), dtype=torch.float16, device="cuda")
