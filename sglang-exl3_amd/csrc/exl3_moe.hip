@@ -35,10 +35,6 @@ int moe_launch(int K, int cb, int ns, const MoeParams& p, hipStream_t st) {
 
 // ------------------------------------------------------------------ routing
 
-struct MoeTables {
-    const int64_t* t[9];  // gate trellis/suh/svh, up ..., down ...
-};
-
 // Group the entries by expert and cut each expert's rows into work units of
 // up to 16 rows, with the expert's nine weight addresses resolved.  Entries
 // with ids outside [0, E) are dropped.  Row order inside an expert follows
@@ -403,8 +399,13 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     __half* yslots = reinterpret_cast<__half*>(w8 + L.y_off);
     int* tok_valid = reinterpret_cast<int*>(w8 + L.tokv_off);
 
+    // One token: every GEMV workgroup maps its unit to a slot of ids itself,
+    // and the routing kernel (a launch, ~3 us in a graph) is left out
+    const bool direct = tokens == 1 && !L.rot && L.gu.kw == 1 && L.dn.kw == 1 &&
+                        (size_t)topk * nblk_max <= kWsMaxCounters && env_int("EXL3_MOE_DIRECT", 1) != 0;
+
     // 1. routing
-    {
+    if (!direct) {
         const size_t smem = moe_route_smem_bytes(E, L.entries, tokens);
         int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&moe_route_kernel), smem, "exl3 moe route");
         if (rc) return rc;
@@ -422,6 +423,10 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     p.limit = limit;
     p.counters = reinterpret_cast<int*>(w8);
     p.partials = reinterpret_cast<float*>(w8 + L.part_off);
+    p.direct = direct;
+    p.ids = ids;
+    p.E = E;
+    p.tabs = tb;
 
     // 2. gate/up input rotation, once per routed row (larger batches)
     __half* xr = reinterpret_cast<__half*>(w8 + L.xr_off);

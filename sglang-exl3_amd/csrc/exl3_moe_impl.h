@@ -35,9 +35,11 @@ namespace exl3 {
 constexpr int MOE_GATE_UP = 0;
 constexpr int MOE_DOWN = 1;
 // Kernel variants (compile-time, so each holds only its own code path):
-constexpr int MV_GU = 0;      // gate/up, input rows rotated by each item
-constexpr int MV_GU_ROT = 1;  // gate/up, input rows arrive rotated per projection
-constexpr int MV_DOWN = 2;    // down, input rows arrive rotated
+constexpr int MV_GU = 0;         // gate/up, input rows rotated by each item
+constexpr int MV_GU_ROT = 1;     // gate/up, input rows arrive rotated per projection
+constexpr int MV_DOWN = 2;       // down, input rows arrive rotated
+constexpr int MV_GU_DIRECT = 3;  // MV_GU for one token routed directly (no routing kernel)
+constexpr int MV_DOWN_DIRECT = 4;  // MV_DOWN for one token routed directly
 constexpr int MOE_ROUTE_THREADS = 1024;
 constexpr int MOE_UNIT_ROWS = 16;  // rows of a work unit: one MFMA row block
 constexpr int MV_PRE = 2;          // rotation blocks per wave whose activations are preloaded
@@ -54,6 +56,12 @@ struct alignas(16) MoeUnit {
     long long pad2;
 };
 static_assert(sizeof(MoeUnit) == 96, "MoeUnit layout");
+
+// Per-expert weight address tables (int64 device arrays indexed by expert id,
+// the layout of src/sglang_exl3/exl3.py:590-607).
+struct MoeTables {
+    const int64_t* t[9];  // gate trellis/suh/svh, up ..., down ...
+};
 
 // Device arrays written by moe_route_kernel (inside the caller's workspace).
 struct MoeRoute {
@@ -93,6 +101,13 @@ struct MoeParams {
     const void* weights;      // [entries] routing weights, fp16 or fp32
     int weights_f16;
     __half* final_out;        // [tokens][n]
+    // One token routed directly, without the routing kernel: unit u is slot u
+    // (one row, compact row u, entry u) with its weights looked up in tabs;
+    // slots whose id is outside [0, E) are skipped.
+    int direct;
+    const int32_t* ids;
+    int E;
+    MoeTables tabs;
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
@@ -129,7 +144,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     extern __shared__ __align__(16) unsigned char mv_smem[];
     __shared__ int is_last;
 
-    const int nunits = uniform_i(gptr(p.rt.counts)[1]);
+    constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
+    const int nunits = direct ? p.topk : uniform_i(gptr(p.rt.counts)[1]);
     const int nblk_n = p.n >> 7;
     const int BPI = p.bx_per_item, ngroups = nblk_n / BPI;
     const int S = p.splits, P = p.proj_launch;
@@ -146,8 +162,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cw = wave & 3, kwi = wave >> 2;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
-    constexpr bool down = MODE == MV_DOWN;
-    constexpr bool pre_rotated = MODE != MV_GU;  // input rows arrive rotated
+    constexpr bool down = MODE == MV_DOWN || MODE == MV_DOWN_DIRECT;
+    constexpr bool pre_rotated = MODE != MV_GU && MODE != MV_GU_DIRECT;  // input rows arrive rotated
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const size_t split_stride = (size_t)p.entries * 128;
 
@@ -158,6 +174,21 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     float* ybuf = xsum + ((ROWS * nblk128 + 3) & ~3);
     if (tid < 8) xs[xs_halves + tid] = (_Float16)0.0f;
     const EXL3_GLOBAL int* rows_g = gptr(p.rt.rows);
+    // one token routed directly: its valid slots (the fused combine's count);
+    // with none, workgroup 0 writes the zero output row
+    int direct_valid = 0;
+    if (down && direct) {
+        for (int sl = 0; sl < p.topk; ++sl) {
+            const int e = uniform_i(gptr(p.ids)[sl]);
+            direct_valid += e >= 0 && e < p.E;
+        }
+        if (direct_valid == 0) {
+            if (blockIdx.x == 0 && p.fc)
+                for (int c = tid; c < n / 2; c += blockDim.x)
+                    reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(p.final_out))[c] = 0u;
+            return;
+        }
+    }
 
     for (int it = blockIdx.x; it < total; it += gridDim.x) {
         const int u = it / per_unit;
@@ -167,14 +198,31 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
         const int pl = rem / S, sidx = rem - pl * S;
         const int proj = p.proj_base + pl;
 
-        const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
-        const int m = uniform_i(ud->nrows), crow0 = uniform_i(ud->crow0);
         const int pb = down ? 6 : 3 * proj;
-        const uint32_t* trellis = reinterpret_cast<const uint32_t*>(uniform_p(ud->ptr[pb]));
-        const void* suh = uniform_p(ud->ptr[pb + 1]);
-        const void* ev0p = uniform_p(ud->ptr[down ? 8 : 2]);  // svh of down / gate
-        const void* ev1p = uniform_p(ud->ptr[5]);                    // svh of up
-        const void* ev2p = uniform_p(ud->ptr[7]);                    // suh of down (its input rotation)
+        int m, crow0;
+        const void *tp, *suh, *ev0p, *ev1p, *ev2p;
+        if (direct) {
+            const int e = uniform_i(gptr(p.ids)[u]);
+            if (e < 0 || e >= p.E) continue;  // skipped slot (uniform over the workgroup)
+            m = 1;
+            crow0 = u;
+            auto tab = [&](int j) { return uniform_p(reinterpret_cast<const void*>(gptr(p.tabs.t[j])[e])); };
+            tp = tab(pb);
+            suh = tab(pb + 1);
+            ev0p = tab(down ? 8 : 2);
+            ev1p = tab(5);
+            ev2p = tab(7);
+        } else {
+            const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
+            m = uniform_i(ud->nrows);
+            crow0 = uniform_i(ud->crow0);
+            tp = uniform_p(ud->ptr[pb]);
+            suh = uniform_p(ud->ptr[pb + 1]);
+            ev0p = uniform_p(ud->ptr[down ? 8 : 2]);  // svh of down / gate
+            ev1p = uniform_p(ud->ptr[5]);             // svh of up
+            ev2p = uniform_p(ud->ptr[7]);             // suh of down (its input rotation)
+        }
+        const uint32_t* trellis = reinterpret_cast<const uint32_t*>(tp);
         const int kt_wg0 = sidx * kts_wg;
         const int kt_w0 = kt_wg0 + kwi * 4 * nsteps;
         const int bx0 = bg * BPI;
@@ -393,7 +441,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                     sum_rows(1, crow, d);
                     float va = d[0].x, vb = d[0].y;
                     fwht128_pair_fast(va, vb, lane);
-                    const int entry = uniform_i(rows_g[crow]);
+                    const int entry = direct ? crow : uniform_i(rows_g[crow]);
                     // the expert's output row in fp16, as the separate linear returns it
                     const __half2 yh = h2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0));
                     if (p.fc) {
@@ -403,7 +451,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
                                 ? __half2float(__ushort_as_half(
                                       gptr(reinterpret_cast<const uint16_t*>(p.weights))[entry]))
                                 : gptr(reinterpret_cast<const float*>(p.weights))[entry];
-                        const int c = uniform_i(gptr(p.tok_valid)[t]);
+                        const int c = direct ? direct_valid : uniform_i(gptr(p.tok_valid)[t]);
                         const FxPair cur =
                             fx_issue_pair(p.acc + (size_t)t * n + c0, wv * __low2float(yh), wv * __high2float(yh));
                         if (ptok >= 0)
@@ -437,7 +485,8 @@ template <int K>
 int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     const size_t smem = moe_smem_bytes(4 * ns * p.kw, p.kw);
     const int threads = 256 * p.kw;
-    const int mv = p.mode == MOE_DOWN ? MV_DOWN : (p.in_rot ? MV_GU_ROT : MV_GU);
+    const int mv = p.mode == MOE_DOWN ? (p.direct ? MV_DOWN_DIRECT : MV_DOWN)
+                                      : (p.in_rot ? MV_GU_ROT : (p.direct ? MV_GU_DIRECT : MV_GU));
 #define EXL3_MV_KW(CBV, NSV, MVV, KWV)                                                                 \
     if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV) {                                          \
         const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV>);       \
@@ -449,7 +498,9 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
         return launch_status("exl3 moe launch");                                                      \
     }
 #define EXL3_MV_NS(CBV, NSV, MVV) EXL3_MV_KW(CBV, NSV, MVV, 1) EXL3_MV_KW(CBV, NSV, MVV, 2)
-#define EXL3_MV_MODES(CBV, NSV) EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)
+#define EXL3_MV_MODES(CBV, NSV)                                                                        \
+    EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)             \
+    EXL3_MV_KW(CBV, NSV, MV_GU_DIRECT, 1) EXL3_MV_KW(CBV, NSV, MV_DOWN_DIRECT, 1)
 #define EXL3_MV_CASE(CBV) \
     EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 16)
     EXL3_MV_CASE(0) EXL3_MV_CASE(1) EXL3_MV_CASE(2)

@@ -251,6 +251,28 @@ def test_moe_fused_combine(T, topk, E, fc_tokens, monkeypatch):
     check_close(o, ex.ref(x, ids, w), f"moe fused combine T={T}")
 
 
+@pytest.mark.parametrize("direct", ["0", "1"])
+@pytest.mark.parametrize("topk,E,invalid,fc_tokens", [(8, 16, 0, 16), (6, 8, 2, 16), (4, 8, 4, 16), (8, 16, 3, 0)])
+def test_moe_one_token_direct_routing(topk, E, invalid, fc_tokens, direct, monkeypatch):
+    """One token: the GEMV workgroups map units to slots themselves (no routing kernel) or use the
+    routing kernel; skipped slots, a token with no valid slot (zero row) and both combine paths."""
+    print(f"case: moe one token topk={topk} E={E} invalid={invalid} fc_tokens={fc_tokens} direct={direct}",
+          flush=True)
+    monkeypatch.setenv("EXL3_MOE_DIRECT", direct)
+    monkeypatch.setenv("EXL3_MOE_FC_TOKENS", str(fc_tokens))
+    ex = Experts(E, 256, 384, (3, 3, 3), 1, seed=70 + topk + invalid)
+    x = make_x(1, 256, seed=71 + topk)
+    ids, w = _routing(1, topk, E, seed=72 + topk + invalid)
+    ids[0, :invalid] = [-1 if j % 2 else E + j for j in range(invalid)]
+    out = _layer_capi(ex, x, ids, w, cb=1)
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    if invalid == topk:
+        assert np.all(o == 0.0)
+    else:
+        check_close(o, ex.ref(x, ids, w), f"moe one token direct={direct}")
+
+
 def test_moe_rejects_bad_arguments():
     ex = Experts(2, 256, 128, (2, 2, 2), 1, seed=1)
     x = torch.zeros((1, 200), dtype=torch.float16, device="cuda")
