@@ -42,11 +42,10 @@ int moe_launch(int K, int cb, int ns, const MoeParams& p, hipStream_t st) {
 // do not depend on it.  Also counts each token's valid slots (the fused
 // combine's completion count) and, when the combine is fused, writes the zero
 // output row of a token without any valid slot.
-__global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int32_t* ids, int entries, int E,
-                                                                     MoeTables tabs, MoeRoute rt, int topk,
-                                                                     int* tok_valid, __half* out, int hidden,
-                                                                     int fc) {
-    extern __shared__ __align__(16) int rt_smem[];
+// (One workgroup of MOE_ROUTE_THREADS threads; rt_smem: moe_route_smem_bytes.)
+__device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, int entries, int E, MoeTables tabs,
+                                            MoeRoute rt, int topk, int* tok_valid, __half* out, int hidden,
+                                            int fc) {
     int* cnt = rt_smem;    // [E]
     int* off = cnt + E;    // [E] first compact row
     int* uoff = off + E;   // [E] first unit
@@ -138,30 +137,45 @@ __global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int3
     }
 }
 
+__global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_kernel(const int32_t* ids, int entries, int E,
+                                                                     MoeTables tabs, MoeRoute rt, int topk,
+                                                                     int* tok_valid, __half* out, int hidden,
+                                                                     int fc) {
+    extern __shared__ __align__(16) int rt_smem[];
+    route_block(rt_smem, ids, entries, E, tabs, rt, topk, tok_valid, out, hidden, fc);
+}
+
 // ------------------------------------------------------------------ rotation
 
-// Input rotation of the gate and up projections, once per routed row:
-// xr[p][crow] = fp16(FWHT(x[token] (.) suh_p[expert]) / sqrt(128)), p = 0 gate,
-// 1 up, rows by compact row.  The GEMV items then stage these rows as they
-// are, instead of rotating the same rows again for every column block they
-// cover.  One wave per (row, projection, 128-block); the operations are the
-// GEMV staging's, so the staged values are the same.
-__global__ __launch_bounds__(256) void moe_rotate_kernel(const __half* x, const int32_t* ids, MoeTables tabs,
-                                                         MoeRoute rt, int topk, int entries, int hidden,
-                                                         __half* xr) {
-    const int nblk = hidden >> 7, per_row = 2 * nblk;
-    const int job = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int crow = job / per_row;
-    if (crow >= gptr(rt.counts)[2]) return;
-    const int rem = job - crow * per_row, proj = rem / nblk, j = rem - proj * nblk;
-    const int entry = gptr(rt.rows)[crow];
+// Input rotation of the gate and up projections, once per (token, slot)
+// entry: xr[p][entry] = fp16(FWHT(x[token] (.) suh_p[expert]) / sqrt(128)),
+// p = 0 gate, 1 up.  The GEMV items then stage these rows as they are,
+// instead of rotating the same rows again for every column block they cover.
+// It needs only ids, so it shares a launch with the routing: workgroup 0
+// routes, the others rotate, one wave per (entry, projection, 128-block);
+// the operations are the GEMV staging's, so the staged values are the same.
+__global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_route_rotate_kernel(
+    const int32_t* ids, int entries, int E, MoeTables tabs, MoeRoute rt, int topk, int* tok_valid, __half* out,
+    int hidden, int fc, const __half* x, __half* xr) {
+    if (blockIdx.x == 0) {
+        extern __shared__ __align__(16) int rt_smem[];
+        route_block(rt_smem, ids, entries, E, tabs, rt, topk, tok_valid, out, hidden, fc);
+        return;
+    }
+    constexpr int WAVES = MOE_ROUTE_THREADS / 64;
+    const int nblk = hidden >> 7, per_entry = 2 * nblk;
+    const int job = (blockIdx.x - 1) * WAVES + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int entry = job / per_entry;
+    if (entry >= entries) return;
     const int e = gptr(ids)[entry];
+    if (e < 0 || e >= E) return;
+    const int rem = job - entry * per_entry, proj = rem / nblk, j = rem - proj * nblk;
     const __half* suh = reinterpret_cast<const __half*>(gptr(tabs.t[proj == 0 ? 1 : 4])[e]);
     const int kg = j * 128 + 2 * lane;
     const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)(entry / topk) * hidden + kg), ld_h2(gptr(suh) + kg));
     float a = __low2float(pr), c = __high2float(pr);
     fwht128_pair_fast(a, c, lane);
-    st_h2(gptr(xr) + ((size_t)proj * entries + crow) * hidden + kg, h2_rn(a * kHadNorm, c * kHadNorm));
+    st_h2(gptr(xr) + ((size_t)proj * entries + entry) * hidden + kg, h2_rn(a * kHadNorm, c * kHadNorm));
 }
 
 // ------------------------------------------------------------------ combine
@@ -307,8 +321,8 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
     return MoePlan{ns, kw, S, bpi};
 }
 
-// Batches of at least this many tokens rotate the gate/up input rows once in a
-// pass of their own (moe_rotate_kernel); below it each GEMV item rotates its
+// Batches of at least this many tokens rotate the gate/up input rows once, in
+// the routing launch (moe_route_rotate_kernel); below it each GEMV item rotates its
 // rows (one row per unit at one token: nothing to share).
 constexpr int kMoeRotTokens = 8;
 constexpr int kMoeFusedCombineTokens = 16;
@@ -404,8 +418,22 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     const bool direct = tokens == 1 && !L.rot && L.gu.kw == 1 && L.dn.kw == 1 &&
                         (size_t)topk * nblk_max <= kWsMaxCounters && env_int("EXL3_MOE_DIRECT", 1) != 0;
 
-    // 1. routing
-    if (!direct) {
+    // 1. routing (with the gate/up input rotation in the same launch for
+    //    larger batches)
+    __half* xr = reinterpret_cast<__half*>(w8 + L.xr_off);
+    if (L.rot) {
+        const size_t smem = moe_route_smem_bytes(E, L.entries, tokens);
+        int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&moe_route_rotate_kernel), smem,
+                                   "exl3 moe route+rotate");
+        if (rc) return rc;
+        const long long jobs = (long long)L.entries * 2 * (hidden / 128);
+        const long long blocks = 1 + (jobs + MOE_ROUTE_THREADS / 64 - 1) / (MOE_ROUTE_THREADS / 64);
+        moe_route_rotate_kernel<<<(unsigned)blocks, MOE_ROUTE_THREADS, smem, st>>>(
+            ids, L.entries, E, tb, rt, topk, tok_valid, reinterpret_cast<__half*>(out), hidden, L.fc,
+            reinterpret_cast<const __half*>(x), xr);
+        rc = launch_status("exl3 moe route+rotate launch");
+        if (rc) return rc;
+    } else if (!direct) {
         const size_t smem = moe_route_smem_bytes(E, L.entries, tokens);
         int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&moe_route_kernel), smem, "exl3 moe route");
         if (rc) return rc;
@@ -427,16 +455,6 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     p.ids = ids;
     p.E = E;
     p.tabs = tb;
-
-    // 2. gate/up input rotation, once per routed row (larger batches)
-    __half* xr = reinterpret_cast<__half*>(w8 + L.xr_off);
-    if (L.rot) {
-        const long long jobs = (long long)L.entries * 2 * (hidden / 128);
-        moe_rotate_kernel<<<(unsigned)((jobs + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x), ids, tb, rt,
-                                                                      topk, L.entries, hidden, xr);
-        const int rc = launch_status("exl3 moe rotate launch");
-        if (rc) return rc;
-    }
 
     // 3. gate + up (+ SwiGLU + down input rotation)
     p.mode = MOE_GATE_UP;

@@ -91,7 +91,7 @@ struct MoeParams {
     int bx_per_item;   // column blocks one item covers (divides n/128)
     int mode;
     int in_rot;        // GATE_UP: x holds the rows already rotated per projection,
-                       // [2][entries][k] by compact row (moe_rotate_kernel)
+                       // [2][entries][k] by (token, slot) entry (moe_route_rotate_kernel)
     // DOWN with the weighted combine fused (fc != 0): each row's w[entry] * y
     // is added into 64-bit fixed-point accumulators acc[token][n]; the add that
     // completes the token's valid-slot count writes the fp16 output and clears
@@ -234,7 +234,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
         if (it != (int)blockIdx.x) __syncthreads();  // the previous item is done with LDS
 
         auto x_row = [&](int row) -> const EXL3_GLOBAL __half* {
-            if (pre_rotated) return gptr(p.x) + ((size_t)(down ? 0 : proj * p.entries) + crow0 + row) * k;
+            if (down) return gptr(p.x) + (size_t)(crow0 + row) * k;
+            if (pre_rotated) return gptr(p.x) + ((size_t)proj * p.entries + rows_g[crow0 + row]) * k;
             if (p.single_token) return gptr(p.x);
             return gptr(p.x) + (size_t)(rows_g[crow0 + row] / p.topk) * k;
         };
