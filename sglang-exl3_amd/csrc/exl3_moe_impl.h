@@ -44,7 +44,7 @@ constexpr int MV_GU_DIRECT = 3;  // MV_GU for one token routed directly (no rout
 constexpr int MV_DOWN_DIRECT = 4;  // MV_DOWN for one token routed directly
 constexpr int MOE_ROUTE_THREADS = 1024;
 constexpr int MOE_UNIT_ROWS = 16;  // rows of a work unit: one MFMA row block
-constexpr int MV_PRE = 2;          // rotation blocks per wave whose activations are preloaded
+constexpr int MV_PRE = 2;          // staged blocks per wave whose activations are loaded up front
 
 // A work unit: up to 16 rows of one expert, with the expert's weight
 // addresses resolved by the routing kernel (one dependent load for the GEMV
@@ -233,15 +233,21 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
         };
         if (it != (int)blockIdx.x) __syncthreads();  // the previous item is done with LDS
 
+        // the entries of the unit's rows, one per lane, looked up once (the
+        // row loops below read them with readlane instead of a dependent load
+        // per row)
+        const bool by_entry = !down && !direct && (pre_rotated || !p.single_token);
+        const int ent_lane = (by_entry && lane < m) ? rows_g[crow0 + lane] : 0;
         auto x_row = [&](int row) -> const EXL3_GLOBAL __half* {
             if (down) return gptr(p.x) + (size_t)(crow0 + row) * k;
-            if (pre_rotated) return gptr(p.x) + ((size_t)proj * p.entries + rows_g[crow0 + row]) * k;
-            if (p.single_token) return gptr(p.x);
-            return gptr(p.x) + (size_t)(rows_g[crow0 + row] / p.topk) * k;
+            if (!by_entry) return gptr(p.x);
+            const int entry = __builtin_amdgcn_readlane(ent_lane, row);
+            if (pre_rotated) return gptr(p.x) + ((size_t)proj * p.entries + entry) * k;
+            return gptr(p.x) + (size_t)(entry / p.topk) * k;
         };
 
-        // 1. activation loads (up to GV_PRE blocks per wave), then the first
-        //    column block's weights
+        // 1. activation loads (up to MV_PRE blocks per wave, all in flight),
+        //    then the first column block's weights
         const int nrot = m * nblk128;
         __half2 xpre[MV_PRE], spre[MV_PRE];
 #pragma unroll
