@@ -51,10 +51,18 @@ __device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, in
     int* uoff = off + E;   // [E] first unit
     int* pos = uoff + E;   // [entries]
     int* tv = pos + entries;  // [tokens] valid slots
-    __shared__ int any_empty;
+    // Work units are ordered heaviest first: every expert's full 16-row units,
+    // then the partial units by row count, descending.  The GEMV kernels take
+    // items in that order (in rounds over the grid), so the costly units start
+    // first and the cheap ones fill the last round.
+    __shared__ int any_empty, rcount[MOE_UNIT_ROWS], rfill[MOE_UNIT_ROWS], rstart[MOE_UNIT_ROWS];
     const int tid = threadIdx.x, tokens = entries / topk;
     for (int e = tid; e < E; e += MOE_ROUTE_THREADS) cnt[e] = 0;
     for (int t = tid; t < tokens; t += MOE_ROUTE_THREADS) tv[t] = 0;
+    if (tid < MOE_UNIT_ROWS) {
+        rcount[tid] = 0;
+        rfill[tid] = 0;
+    }
     if (tid == 0) any_empty = 0;
     __syncthreads();
     const EXL3_GLOBAL int32_t* idg = gptr(ids);
@@ -69,6 +77,10 @@ __device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, in
         gptr(tok_valid)[t] = tv[t];
         if (tv[t] == 0) any_empty = 1;
     }
+    for (int e = tid; e < E; e += MOE_ROUTE_THREADS) {
+        const int r = cnt[e] % MOE_UNIT_ROWS;
+        if (r) atomicAdd(&rcount[r], 1);
+    }
     __syncthreads();
     if (fc && any_empty) {
         const int hp = hidden >> 1;  // fp16 pairs per row
@@ -77,7 +89,7 @@ __device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, in
             if (tv[t] == 0) reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(out) + (size_t)t * hidden)[idx - t * hp] = 0u;
         }
     }
-    // exclusive scans over the experts (rows, units, active), one wave
+    // exclusive scans over the experts (rows, full units, active), one wave
     if (tid < 64) {
         const int chunk = (E + 63) / 64;
         const int e0 = tid * chunk, e1 = min(E, e0 + chunk);
@@ -85,7 +97,7 @@ __device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, in
         for (int e = e0; e < e1; ++e) {
             const int c = cnt[e];
             sr += c;
-            su += (c + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
+            su += c / MOE_UNIT_ROWS;
             sa += c > 0;
         }
         int ir = sr, iu = su, ia = sa;  // inclusive wave scans
@@ -101,14 +113,20 @@ __device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, in
         int r = ir - sr, uu = iu - su;
         for (int e = e0; e < e1; ++e) {
             off[e] = r;
-            uoff[e] = uu;
+            uoff[e] = uu;  // first full unit
             r += cnt[e];
-            uu += (cnt[e] + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
+            uu += cnt[e] / MOE_UNIT_ROWS;
         }
         if (tid == 63) {
+            // partial units after the iu full ones, by row count descending
+            int start = iu;
+            for (int rr = MOE_UNIT_ROWS - 1; rr >= 1; --rr) {
+                rstart[rr] = start;
+                start += rcount[rr];
+            }
             gptr(rt.counts)[0] = ia;
-            gptr(rt.counts)[1] = iu;
-            gptr(rt.counts)[2] = ir;  // routed rows
+            gptr(rt.counts)[1] = start;  // work units
+            gptr(rt.counts)[2] = ir;     // routed rows
         }
     }
     __syncthreads();
@@ -125,12 +143,13 @@ __device__ __forceinline__ void route_block(int* rt_smem, const int32_t* ids, in
         ud.pad2 = 0;
 #pragma unroll
         for (int j = 0; j < 9; ++j) ud.ptr[j] = reinterpret_cast<const void*>(gptr(tabs.t[j])[e]);
-        const int nu = (c + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS;
+        const int nu = (c + MOE_UNIT_ROWS - 1) / MOE_UNIT_ROWS, nfull = c / MOE_UNIT_ROWS;
         for (int ch = 0; ch < nu; ++ch) {
             ud.nrows = min(MOE_UNIT_ROWS, c - ch * MOE_UNIT_ROWS);
             ud.crow0 = off[e] + ch * MOE_UNIT_ROWS;
+            const int slot = ch < nfull ? uoff[e] + ch : rstart[ud.nrows] + atomicAdd(&rfill[ud.nrows], 1);
             const u32x4_t* src = reinterpret_cast<const u32x4_t*>(&ud);
-            EXL3_GLOBAL u32x4_t* dst = reinterpret_cast<EXL3_GLOBAL u32x4_t*>(gptr(rt.units) + uoff[e] + ch);
+            EXL3_GLOBAL u32x4_t* dst = reinterpret_cast<EXL3_GLOBAL u32x4_t*>(gptr(rt.units) + slot);
 #pragma unroll
             for (int j = 0; j < (int)(sizeof(MoeUnit) / 16); ++j) dst[j] = src[j];
         }

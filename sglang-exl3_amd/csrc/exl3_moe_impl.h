@@ -192,7 +192,11 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
         }
     }
 
-    for (int it = blockIdx.x; it < total; it += gridDim.x) {
+    // Items in rounds over the grid, snake order (round r: workgroup b takes
+    // item r G + b for even r, r G + G - 1 - b for odd r), so the workgroup with
+    // the last (lightest) item of a round takes the first (heaviest) of the next.
+    const int G = gridDim.x, b0 = blockIdx.x;
+    for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0)) {
         const int u = it / per_unit;
         int rem = it - u * per_unit;
         const int bg = rem / (P * S);
