@@ -216,6 +216,28 @@ __device__ __forceinline__ void prime_weights(uint32_t (&w)[gv_depth<K>()][K], c
     for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < last ? d : last) * step_stride, w[d]);
 }
 
+// One MFMA B fragment (values u = 4F..4F+3 of the lane's group, pair form)
+// into every row block's accumulator for its column tile (Q = F / 2, c = F % 2).
+template <int K, int CB, int MB, int F>
+__device__ __forceinline__ void mv_frag(const uint32_t* buf, const uint32_t* mid, const half8_t (&A)[MB][4],
+                                        float4_t (&acc)[MB][2]) {
+    uint32_t vf[4];
+    vf[0] = decode_pair_word<CB>(window_mid<K, 4 * F + 0>(buf, mid));
+    vf[1] = decode_pair_word<CB>(window_mid<K, 4 * F + 1>(buf, mid));
+    vf[2] = decode_pair_word<CB>(window_mid<K, 4 * F + 2>(buf, mid));
+    vf[3] = decode_pair_word<CB>(window_mid<K, 4 * F + 3>(buf, mid));
+    const half8_t B = *reinterpret_cast<const half8_t*>(vf);
+    constexpr int Q = F >> 1, c = F & 1;
+#pragma unroll
+    for (int rb = 0; rb < MB; ++rb) acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb][Q], B, acc[rb][c], 0, 0, 0);
+}
+
+template <int K, int CB, int MB, int... Fs>
+__device__ __forceinline__ void mv_frags(const uint32_t* buf, const uint32_t* mid, const half8_t (&A)[MB][4],
+                                         float4_t (&acc)[MB][2], std::integer_sequence<int, Fs...>) {
+    (mv_frag<K, CB, MB, Fs>(buf, mid, A, acc), ...);
+}
+
 // The wave's NS steps: decode 4 k-slices x 2 column tiles per step into MFMA B
 // fragments and multiply with the staged activations.  Software-pipelined and
 // fully unrolled: each step decodes its words, then reuses their registers to
@@ -243,9 +265,6 @@ __device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[gv_depth<K>()][K
 #pragma unroll
         for (int j = 0; j < K; ++j) buf[1 + j] = w[d][j];
         buf[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(prev_addr, (int)buf[K]);
-        uint32_t v[32];
-        decode_group_pairs<K, CB>(buf, v);
-        if (s + D < NS) load_words<K>(tb + (size_t)(s + D) * step_stride, w[d]);
 #pragma unroll
         for (int rb = 0; rb < MB; ++rb)
             if (a_live[rb]) {
@@ -253,17 +272,14 @@ __device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[gv_depth<K>()][K
                 for (int Q = 0; Q < 4; ++Q)
                     A[rb][Q] = *reinterpret_cast<const half8_t*>(a_base[rb] + (s * 16 + Q) * 8);
             }
+        uint32_t mid[K];
 #pragma unroll
-        for (int Q = 0; Q < 4; ++Q) {
-#pragma unroll
-            for (int rb = 0; rb < MB; ++rb) {
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const half8_t B = *reinterpret_cast<const half8_t*>(&v[8 * Q + 4 * c]);
-                    acc[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb][Q], B, acc[rb][c], 0, 0, 0);
-                }
-            }
-        }
+        for (int j = 0; j < K; ++j) mid[j] = __builtin_amdgcn_alignbit(buf[j], buf[j + 1], 16);
+        // fragment by fragment (4 words, then its MFMAs), so only one
+        // fragment's words are live; each accumulator still takes the
+        // quarters Q = 0..3 in order
+        mv_frags<K, CB, MB>(buf, mid, A, acc, std::make_integer_sequence<int, 8>{});
+        if (s + D < NS) load_words<K>(tb + (size_t)(s + D) * step_stride, w[d]);
     }
 }
 
