@@ -341,9 +341,12 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
 }
 
 // Batches of at least this many tokens rotate the gate/up input rows once, in
-// the routing launch (moe_route_rotate_kernel); below it each GEMV item rotates its
-// rows (one row per unit at one token: nothing to share).
-constexpr int kMoeRotTokens = 8;
+// the routing launch (moe_route_rotate_kernel); a single token (no routing
+// launch) has each GEMV item rotate its row.  In the routing launch the
+// rotation costs no launch of its own, and it measured faster from two tokens
+// on (config 4 B = 2 / 4: 27.9 / 29.4 -> 27.3 / 28.5 us; config 5 K = 2, B = 4:
+// 109.0 -> 106.0 us; K = 4: 119.2 -> 115.1 us).
+constexpr int kMoeRotTokens = 2;
 constexpr int kMoeFusedCombineTokens = 16;
 
 struct MoeLayout {
