@@ -318,7 +318,16 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
     const double grid = 512.0;
     int kw = env_int("EXL3_MOE_KW", 1);
     if (kw != 1 && kw != 2) kw = 1;
-    int ns = env_int("EXL3_MOE_NSTEPS", 8);
+    // 12-step items (48 k-slices) when k allows and the pass has work for
+    // 1.5 rounds of the ~1024-workgroup grid even so: fewer splits, so fewer
+    // hand-offs and partial sums (down pass, config 4 B = 64: 98.9 -> 92.6 us,
+    // config 5 K = 2: 109.1 -> 103.9 us; with less work the fewer, longer items
+    // leave workgroups idle: config 4 B = 16: 49.9 -> 54.2 us)
+    int ns = env_int(nproj == 1 ? "EXL3_MOE_DN_NSTEPS" : "EXL3_MOE_GU_NSTEPS", 0);
+    if (ns == 0 && kw == 1 && kslices % 48 == 0 && units * nblk * (kslices / 48) >= 1536.0) ns = 12;
+    if (ns == 12 && kslices % (4 * ns * kw) == 0 && moe_smem_bytes(4 * ns * kw, kw) <= kMaxLds / 2 - 1024)
+        return MoePlan{ns, kw, kslices / (4 * ns * kw), 1};
+    if (ns <= 0 || ns == 12) ns = env_int("EXL3_MOE_NSTEPS", 8);
     while (ns > 2 && (kslices % (4 * ns * kw) || (4 * ns * kw) % 8 ||
                       moe_smem_bytes(4 * ns * kw, kw) > kMaxLds / 2 - 1024))
         ns /= 2;

@@ -515,7 +515,7 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)             \
     EXL3_MV_KW(CBV, NSV, MV_GU_DIRECT, 1) EXL3_MV_KW(CBV, NSV, MV_DOWN_DIRECT, 1)
 #define EXL3_MV_CASE(CBV) \
-    EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 16)
+    EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 12) EXL3_MV_MODES(CBV, 16)
     EXL3_MV_CASE(0) EXL3_MV_CASE(1) EXL3_MV_CASE(2)
 #undef EXL3_MV_CASE
 #undef EXL3_MV_MODES

@@ -273,6 +273,22 @@ def test_moe_one_token_direct_routing(topk, E, invalid, fc_tokens, direct, monke
         check_close(o, ex.ref(x, ids, w), f"moe one token direct={direct}")
 
 
+@pytest.mark.parametrize("T,inter,fc_tokens", [(20, 768, 100), (20, 1536, 0), (3, 768, 16)])
+def test_moe_down_twelve_step_items(T, inter, fc_tokens, monkeypatch):
+    """Down pass with 12-step items (48 k-slices: one split at inter 768, two at 1536), forced
+    by env, with either combine path."""
+    print(f"case: moe down 12-step items T={T} inter={inter} fc_tokens={fc_tokens}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_DN_NSTEPS", "12")
+    monkeypatch.setenv("EXL3_MOE_FC_TOKENS", str(fc_tokens))
+    E, topk = 8, 4
+    ex = Experts(E, 256, inter, (3, 3, 3), 1, seed=60 + T)
+    x = make_x(T, 256, seed=61 + T)
+    ids, w = _routing(T, topk, E, seed=62 + T, invalid=2)
+    out = _layer_capi(ex, x, ids, w, cb=1)
+    torch.cuda.synchronize()
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), f"moe down 12 steps T={T} inter={inter}")
+
+
 def test_moe_rejects_bad_arguments():
     ex = Experts(2, 256, 128, (2, 2, 2), 1, seed=1)
     x = torch.zeros((1, 200), dtype=torch.float16, device="cuda")
