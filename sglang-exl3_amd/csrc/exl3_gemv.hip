@@ -69,7 +69,7 @@ struct GemvPlan {
     int nsteps;  // steps of 4 k-slices per wave
     int kw;      // k waves per workgroup
     int splits;  // workgroups along k
-    int sk;      // 1: balanced kernel (gemv_sk_kernel, m = 1): splits = pieces per column block, nsteps = piece length
+    int sk;      // 1: balanced kernel (gemv_sk_kernel, m <= 4): splits = pieces per column block, nsteps = piece length
 };
 
 int env_int(const char* name, int dflt) {
@@ -84,7 +84,7 @@ int env_int(const char* name, int dflt) {
 // and take the first shape that puts at least `target` waves on the device
 // (1024 SIMDs: ~3 waves each hide HBM and MFMA latency); this also keeps the
 // number of cross-workgroup k-splits (the costly reduction) minimal.
-// Balanced kernel shape (m = 1): P equal pieces per 128-column block, P a
+// Balanced kernel shape (m <= 4): P equal pieces per 128-column block, P a
 // divisor of k/64 with an instantiated piece length.  Cost model fitted to
 // graph-timed sweeps on MI355X (k x n from 2048 x 6144 to 14336 x 4096):
 // with W = ceil(workgroups / CUs) workgroups on the busiest CU and `steps`
@@ -98,9 +98,18 @@ int env_int(const char* name, int dflt) {
 // against 13.7 / 20.1 us; the extra launch and the m x n x P fixed-point adds
 // outweigh the balance).  Returns false when the balanced kernel does not
 // apply.
+// Rows up to which the balanced kernel is used (env EXL3_GEMV_SK_ROWS, up to
+// 4).  Against the k-split kernel on config 2: m = 2: 13.4 -> 11.9 us;
+// m = 3: 14.5 -> 14.7 us; m = 4: 15.2 -> 16.4 us (each row adds its input
+// rotation to every workgroup and an epilogue wave).
+constexpr int kSkMaxRows = 2;
+constexpr int kSkInstRows = 4;
+
 bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {
-    if (experts != 1 || m != 1 || env_int("EXL3_GEMV_SK", 1) == 0) return false;
-    if ((size_t)n * 8 > kWsAccBytes) return false;
+    const int max_rows = env_int("EXL3_GEMV_SK_ROWS", kSkMaxRows);
+    if (experts != 1 || m > (max_rows < kSkInstRows ? max_rows : kSkInstRows) || env_int("EXL3_GEMV_SK", 1) == 0)
+        return false;
+    if ((size_t)m * n * 8 > kWsAccBytes) return false;
     const int ks_blk = k / 64;
     const long long nblk = n / 128;
     const int forced = env_int("EXL3_GEMV_SK_P", 0);
@@ -112,7 +121,7 @@ bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {
         const int ns = ks_blk / P;
         bool inst = false;
         for (int c : kSkSteps) inst |= c == ns;
-        if (!inst || gemv_sk_smem_bytes(ns) > kMaxGemvSmem) continue;
+        if (!inst || gemv_sk_smem_bytes(ns, gemv_sk_rows(m)) > kMaxGemvSmem) continue;
         const long long W = (nblk * P + cus - 1) / cus;
         const double cost = 0.242 * (double)(W * ns) + 0.089 * (double)W + 0.902 / (double)(W < 4 ? W : 4);
         if (cost < best_cost - 1e-9) {
@@ -161,7 +170,7 @@ GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
 }
 
 size_t workspace_bytes_for(const GemvPlan& pl, int m, int n, int experts) {
-    if (pl.sk) return kWsAccOffset + (size_t)n * 8;
+    if (pl.sk) return kWsAccOffset + (size_t)m * n * 8;
     if (pl.splits <= 1) return 0;
     const size_t nblk = (size_t)(n / 128) * experts;
     return kWsScratchOffset + nblk * pl.splits * (size_t)m * 128 * sizeof(float);
@@ -190,6 +199,7 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
         q.svh = p.svh;
         q.y = p.y;
         q.acc = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + kWsAccOffset);
+        q.m = p.m;
         q.k = p.k;
         q.n = p.n;
         q.pieces = pl.splits;
@@ -248,7 +258,7 @@ extern "C" int exl3_gemv_plan(int m, int k, int n, int K, int experts, int* out)
     out[1] = pl.nsteps;
     out[2] = pl.kw;
     out[3] = pl.splits;
-    out[4] = (int)(pl.sk ? gemv_sk_smem_bytes(pl.nsteps) : gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw));
+    out[4] = (int)(pl.sk ? gemv_sk_smem_bytes(pl.nsteps, gemv_sk_rows(m)) : gemv_smem_bytes(mc, 4 * pl.nsteps * pl.kw, pl.kw));
     return EXL3_OK;
 }
 

@@ -65,6 +65,7 @@ def test_batched_rejects_bad_arguments():
 
 
 SK_STEPS = (1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16)
+SK_MAX_ROWS = 2  # rows served by the balanced kernel (kSkMaxRows in csrc/exl3_gemv.hip)
 
 
 def _check_plan(m, k, n, K, experts=1):
@@ -72,9 +73,10 @@ def _check_plan(m, k, n, K, experts=1):
     assert _lib.lib().exl3_gemv_plan(m, k, n, K, experts, out) == 0
     mb, ns, kw, splits, lds = list(out)
     assert 16 * mb >= m and 0 < lds <= 160 * 1024
-    balanced = experts == 1 and m == 1 and n * 8 <= 4 * 1024 * 1024 and os.environ.get("EXL3_GEMV_SK") != "0"
+    balanced = (experts == 1 and m <= SK_MAX_ROWS and m * n * 8 <= 4 * 1024 * 1024
+                and os.environ.get("EXL3_GEMV_SK") != "0")
     if balanced:
-        # balanced bs=1 kernel: each column block's k/64 k-steps in `splits` equal pieces of ns steps
+        # balanced kernel: each column block's k/64 k-steps in `splits` equal pieces of ns steps
         ks_blk = k // 64
         assert kw == 1 and 1 <= splits <= min(63, ks_blk) and ks_blk % splits == 0
         assert ns == ks_blk // splits and ns in SK_STEPS

@@ -197,6 +197,38 @@ def test_gemv_balanced_pieces(k, n, K, cb, pieces):
     assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
 
 
+@pytest.mark.parametrize("m,k,n,K,cb,pieces", [
+    (2, 512, 384, 4, 1, 2), (3, 768, 256, 3, 2, 3), (4, 1024, 256, 4, 0, 16), (4, 4096, 256, 2, 1, 8),
+    (2, 2048, 128, 5, 2, 32), (3, 640, 640, 4, 1, 10),
+])
+def test_gemv_balanced_rows(m, k, n, K, cb, pieces):
+    """Balanced kernel with 2..4 rows (A rows 0..m-1, one epilogue wave per row) at forced piece
+    counts; a second call gives the same bits and the workspace zero regions are zero again."""
+    print(f"case: balanced gemv rows m={m} k={k} n={n} K={K} cb={cb} pieces={pieces}", flush=True)
+    trellis, suh, svh = make_weight(k, n, K, seed=750 + m + pieces + 3 * K + cb)
+    x = make_x(m, k, seed=751 + m + pieces)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    env = {"EXL3_GEMV_SK_P": pieces, "EXL3_GEMV_SK_ROWS": 4}
+    plan = _with_env(env, lambda: _plan(m, k, n, K))
+    assert plan[1] == (k // 64) // pieces and plan[2] == 1 and plan[3] == pieces
+    L = _lib.lib()
+    need = int(L.exl3_gemv_workspace_size(m, k, n, K, 1))
+    assert need >= 256 * 1024 + m * n * 8
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    ys = []
+    for _ in range(2):
+        y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+        rc = _with_env(env, lambda: L.exl3_gemv(xd.data_ptr(), tr.data_ptr(), su.data_ptr(), sv.data_ptr(),
+                                                 y.data_ptr(), m, k, n, K, cb, ws.data_ptr(), ws.numel(),
+                                                 int(torch.cuda.current_stream().cuda_stream)))
+        _lib.check(rc, "exl3_gemv")
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(ws)) == 0
+        ys.append(y)
+    check_close(ys[0].float().cpu().numpy(), _oracle_ref(x, trellis, suh, svh, K, cb), f"balanced rows m={m}")
+    assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
+
+
 def _plan(m, k, n, K):
     import ctypes
     out = (ctypes.c_int * 5)()
@@ -221,7 +253,7 @@ def test_gemv_balanced_leaves_accumulators_zero():
     """Every output element's fixed-point accumulator is cleared by the workgroup that
     completes it, so the workspace's zero regions are zero after each call."""
     m, k, n, K = 1, 1024, 2048, 4
-    assert _plan(m, k, n, K)[2] == 1  # the balanced kernel serves m = 1
+    assert _plan(m, k, n, K)[2] == 1  # the balanced kernel serves m <= 2
     trellis, suh, svh = make_weight(k, n, K, seed=900)
     x = make_x(m, k, seed=901)
     xd, tr, su, sv = to_dev(x, trellis, suh, svh)
