@@ -91,9 +91,9 @@ int env_int(const char* name, int dflt) {
 // k-steps on it,
 //   time ~ 0.242 us * steps + 0.089 us * W + 0.902 us / min(W, 4)
 // (per-step work, per-workgroup overhead, and the latency that fewer than
-// four workgroups per CU leave exposed).  From m = 2 on the k-split kernel is
-// used: the balanced kernel's per-workgroup input rotation grows with m
-// (measured at m = 2, 4, 8), and a variant fed by a separate row-rotation pass
+// four workgroups per CU leave exposed).  Above kSkMaxRows rows the k-split
+// kernel is used: the balanced kernel's per-workgroup input rotation and
+// epilogue grow with m, and a variant fed by a separate row-rotation pass
 // was slower too at every piece count (config 2, m = 2 / 8: 14.7 / 23.4 us
 // against 13.7 / 20.1 us; the extra launch and the m x n x P fixed-point adds
 // outweigh the balance).  Returns false when the balanced kernel does not
