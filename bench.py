@@ -32,7 +32,7 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 K_DIM, N_DIM, BITS = 4096, 14336, 4
 NCOPY = 12
-GEMV_WARM_S = 0.2  # untimed warm replay time before each timed GEMV replay
+WARM_S = 0.2  # untimed warm replay time before each timed graph replay
 
 
 def make_weight(k, n, K, seed):
@@ -41,6 +41,18 @@ def make_weight(k, n, K, seed):
     suh = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
     svh = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
     return trellis, suh, svh
+
+
+def _warm_replays(torch, graph):
+    """Untimed replays of `graph` for WARM_S seconds: the GPU's clocks settle
+    under a load only after a few hundred milliseconds (a timed replay right
+    after one warm replay read ~10 % slower than later ones)."""
+    t_end = time.perf_counter() + WARM_S
+    while True:
+        graph.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() >= t_end:
+            break
 
 
 def gemv_timing(torch, L, weights, m, steps, warmup):
@@ -72,15 +84,7 @@ def gemv_timing(torch, L, weights, m, steps, warmup):
             for c in range(steps):
                 launch(c)
     torch.cuda.synchronize()
-    # warm replays for ~0.2 s (untimed): the GPU's clocks settle under this
-    # load only after a few hundred milliseconds (a first timed replay right
-    # after one warm replay read ~10 % slower than later ones)
-    t_warm = time.perf_counter() + GEMV_WARM_S
-    while True:
-        graph.replay()
-        torch.cuda.synchronize()
-        if time.perf_counter() >= t_warm:
-            break
+    _warm_replays(torch, graph)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         e0.record(stream)
@@ -198,8 +202,7 @@ def moe_bench(torch, steps):
                 for c in range(n):
                     layer(c)
         torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
+        _warm_replays(torch, graph)
         with torch.cuda.stream(stream):
             e0.record(stream)
             graph.replay()
@@ -278,8 +281,7 @@ def _graph_time(torch, stream, launch, reps):
             for c in range(reps):
                 launch(c)
     torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
+    _warm_replays(torch, graph)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         e0.record(stream)
