@@ -8,7 +8,8 @@ MCG codebook, m=1) on seeded random trellis tiles and +-1 sign vectors.  The
 calls cycle through 12 distinct weight copies (352 MB, more than the 256 MB
 Infinity Cache) so every step streams its weight from HBM.  The K timed steps
 are one HIP graph of K launches (no host overhead between kernels), bracketed
-by HIP events on the launch stream.  `value` = packed weight bytes per call /
+by HIP events on the launch stream, after W eager warmup launches and 0.2 s of
+untimed replays of the same graph (steady clocks).  `value` = packed weight bytes per call /
 time per call.  Extra fields: the m = 2/4/8 sweep and the CPU baseline (the
 reference's CPU GEMV path restated in oracle/: truncating dequant + fp32
 GEMM, single thread) timed on the host.
