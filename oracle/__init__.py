@@ -232,15 +232,26 @@ def moe_ref(x: np.ndarray, topk_ids: np.ndarray, topk_w: np.ndarray, experts: li
     ids = np.asarray(topk_ids)
     w = np.asarray(topk_w, dtype=np.float32)
     x16 = np.ascontiguousarray(x, dtype=np.float16)
+    used = [e for e in sorted(set(int(i) for i in ids.reshape(-1))) if 0 <= e < len(experts)]
+    # the dequants are independent C calls (ctypes releases the GIL): run them
+    # on a few threads, then the loop below in expert order as before
+    jobs = [(e, p) for e in used for p in ("gate", "up", "down")]
+
+    def _dq(job):
+        e, p = job
+        spec = experts[e][p]
+        return dequant(*spec[:3], spec[3], spec[4], rtz=True)
+
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(max_workers=max(1, min(16, os.cpu_count() or 1))) as ex:
+        mats = list(ex.map(_dq, jobs))
     cache = {}
-    for e in sorted(set(int(i) for i in ids.reshape(-1))):
-        if e < 0 or e >= len(experts):
-            continue
+    for (e, p), W in zip(jobs, mats):
+        cache.setdefault(e, {})[p] = W
+    for e in used:
         tok, slot = np.nonzero(ids == e)
         h = x16[tok]
-        if e not in cache:
-            cache[e] = {p: dequant(*experts[e][p][:3], experts[e][p][3], experts[e][p][4], rtz=True)
-                        for p in ("gate", "up", "down")}
         Wg, Wu, Wd = cache[e]["gate"], cache[e]["up"], cache[e]["down"]
         g = matmul(h, Wg)
         u = matmul(h, Wu)

@@ -145,10 +145,12 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 
 // Prefill path of exl3_gemm (m > 64).  Scratch after the workspace's zeroed
 // regions (shared with the GEMV kernels, which need them to stay zero):
-// [counters][accumulators][xr fp16 m*k][out fp32 m*n].
+// [counters][accumulators][xr fp16 m*k][out fp32 m*n, only when the plan
+// splits k; an unsplit GEMM stores fp16 straight to y].
 size_t fat_xr_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
 size_t fat_gemm_scratch_bytes(int m, int k, int n) {
-    return kWsScratchOffset + fat_xr_bytes(m, k) + (size_t)m * n * 4;
+    const bool split = plan_fat(m, k, n).splits > 1;
+    return kWsScratchOffset + fat_xr_bytes(m, k) + (split ? (size_t)m * n * 4 : 0);
 }
 
 int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,

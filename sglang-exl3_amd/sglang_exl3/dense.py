@@ -38,26 +38,16 @@ def _marker_on(t: Optional[torch.Tensor]) -> bool:
 
 def linear_forward(x2: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
                    codebook: int) -> torch.Tensor:
-    """fp16 [rows, n] = x2 (fp16 [rows, k]) @ W through exl3_gemv / exl3_gemm; any codebook id."""
-    from .ops import workspace
+    """fp16 [rows, n] = x2 (fp16 [rows, k]) @ W for any codebook id, through the
+    registered op torch.ops.sglang_exl3.exl3_linear (exl3_gemv up to 64 rows,
+    exl3_gemm above; shapes checked there), so the call stays one traceable
+    op under torch.compile and graph capture."""
+    from .ops import register_custom_ops
 
+    register_custom_ops()
     if not x2.is_cuda:
         raise RuntimeError("EXL3 linear requires HIP device tensors")
-    rows, k = int(x2.shape[0]), int(x2.shape[1])
-    n = int(trellis.shape[1]) * 16
-    y = torch.empty((rows, n), dtype=torch.float16, device=x2.device)
-    if rows == 0:
-        return y
-    L = _lib.lib()
-    with torch.cuda.device(x2.device):
-        need = int(L.exl3_gemm_workspace_size(rows, k, n, int(K)))
-        ws = workspace(x2.device, need) if need else None
-        fn = L.exl3_gemv if rows <= 64 else L.exl3_gemm
-        rc = fn(x2.data_ptr(), trellis.data_ptr(), suh.data_ptr(), svh.data_ptr(), y.data_ptr(), rows, k, n, int(K),
-                int(codebook), 0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
-                int(torch.cuda.current_stream(x2.device).cuda_stream))
-    _lib.check(rc, "exl3 linear")
-    return y
+    return torch.ops.sglang_exl3.exl3_linear(x2, trellis, suh, svh, int(K), int(codebook))
 
 
 class EXL3DenseLinear:

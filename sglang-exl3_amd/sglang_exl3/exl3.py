@@ -153,29 +153,40 @@ def storage_kind_for_prefix(kinds: dict[str, str], prefix: str) -> Optional[str]
     return child.pop() if child else None
 
 
-def _narrow_tp(t: torch.Tensor, dim: int, rank: int, size: int) -> torch.Tensor:
+def _narrow_tp(t: torch.Tensor, dim: int, rank: int, size: int, align: int) -> torch.Tensor:
+    """Slice `rank` of `size` equal shards along `dim`.  Each shard must be a
+    multiple of `align` elements: 128 features (8 trellis tiles), because the
+    output rotation of every kernel works on whole 128-wide blocks.  The
+    reference checks divisibility only (src/sglang_exl3/exl3.py:347-356); an
+    unaligned split is refused here at load time instead of failing at apply."""
     if size <= 1:
         return t
     n = int(t.shape[dim])
     if n % size:
         raise ValueError(f"EXL3 TP shard: dim {dim} size {n} is not divisible by tp={size}")
     c = n // size
+    if c % align:
+        raise ValueError(f"EXL3 TP shard: dim {dim} size {n} over tp={size} gives {c} per rank, not a multiple "
+                         f"of {align} ({'trellis tiles' if align == 8 else 'features'}; the 128-wide Hadamard "
+                         "blocks cannot be split)")
     return t.narrow(dim, c * rank, c).contiguous()
 
 
 def shard_exl3_col(loaded: torch.Tensor, suffix: str, tp_rank: int, tp_size: int) -> torch.Tensor:
     """Column-parallel (gate/up): trellis splits on its output-tile dim, svh with it."""
     if suffix == "trellis":
-        return _narrow_tp(loaded, 1, tp_rank, tp_size)
+        return _narrow_tp(loaded, 1, tp_rank, tp_size, 8)
     if suffix == "svh":
-        return _narrow_tp(loaded, 0, tp_rank, tp_size)
+        return _narrow_tp(loaded, 0, tp_rank, tp_size, 128)
     return loaded.contiguous()
 
 
 def shard_exl3_row(loaded: torch.Tensor, suffix: str, tp_rank: int, tp_size: int) -> torch.Tensor:
     """Row-parallel (down): trellis splits on its input-tile dim, suh with it."""
-    if suffix in ("trellis", "suh"):
-        return _narrow_tp(loaded, 0, tp_rank, tp_size)
+    if suffix == "trellis":
+        return _narrow_tp(loaded, 0, tp_rank, tp_size, 8)
+    if suffix == "suh":
+        return _narrow_tp(loaded, 0, tp_rank, tp_size, 128)
     return loaded.contiguous()
 
 

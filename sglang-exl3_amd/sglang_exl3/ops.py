@@ -35,6 +35,10 @@ OP_NAMES = (
 # ---------------------------------------------------------------- plumbing
 
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+# Buffers replaced by a larger one.  A HIP graph captured earlier may still
+# hold their addresses, so they are never freed (a replay would otherwise
+# write counters and partial sums into memory that another tensor owns).
+_RETIRED_WORKSPACES: list = []
 
 
 def _stream_ptr(t: torch.Tensor) -> int:
@@ -55,14 +59,35 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Zero-initialised scratch keyed by (device, current stream).  Kernels
     leave their counters zero after each call, so the buffer is reused as is;
     growth allocates a new zeroed buffer (stream-ordered, like the reference's
-    per-stream workspace in src/sglang_exl3/dense.py:45-58)."""
+    per-stream workspace in src/sglang_exl3/dense.py:45-58) and keeps the old
+    one alive for graphs that captured it.
+
+    Growth is refused while the stream is being captured: the zero fill would
+    then only run at graph replay, and eager calls on the stream would find
+    an uninitialised buffer.  Run each op shape once before capture."""
     key = (device.index or 0, int(torch.cuda.current_stream(device).cuda_stream))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"sglang_exl3: the workspace of this stream must grow to {nbytes} bytes during HIP graph "
+                "capture; run the op once (same shape) on this stream before capturing")
         size = max(nbytes, 1 << 20, 0 if ws is None else 2 * ws.numel())
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def check_ws(rc: int, what: str, ws) -> None:
+    """Raise for a non-zero status after re-zeroing the workspace the call
+    used: a call that failed after some of its launches were enqueued can
+    leave split-k counters or fixed-point accumulators non-zero, and every
+    later call on the stream relies on them being zero."""
+    if rc != _lib.EXL3_OK and ws is not None and not torch.cuda.is_current_stream_capturing():
+        ws.zero_()
+    _lib.check(rc, what)
 
 
 def _check_trellis(name: str, trellis: torch.Tensor, K: int) -> None:
@@ -100,7 +125,9 @@ def dequant_trellis_impl(trellis, suh, svh, bits, mcg):
     return W
 
 
-def _gemv_like(name, fn, x, trellis, suh, svh, K, mcg, max_rows=None):
+def _gemv_like(name, fn, x, trellis, suh, svh, K, cb, max_rows=None):
+    """y (fp16 [rows, n]) = x (fp16 [..., k]) @ W through `fn` (exl3_gemv or
+    exl3_gemm); every shape the kernels trust is checked here first."""
     _require_device(name, x, trellis, suh, svh)
     _check_trellis(name, trellis, K)
     if x.dim() < 2:
@@ -111,31 +138,47 @@ def _gemv_like(name, fn, x, trellis, suh, svh, K, mcg, max_rows=None):
         raise RuntimeError(f"sglang_exl3::{name}: x feature dimension does not match trellis")
     if max_rows is not None and not (1 <= m <= max_rows):
         raise RuntimeError(f"sglang_exl3::{name}: native GEMV supports 1 <= m <= {max_rows} (m={m})")
+    if cb not in (_lib.CB_3INST, _lib.CB_MCG, _lib.CB_MUL1):
+        raise RuntimeError(f"sglang_exl3::{name}: codebook id {cb} outside 0..2")
     x2 = _f16(name, x, "x").reshape(m, kdim)
     n = int(trellis.shape[1]) * 16
     suh = _f16(name, suh, "suh")
     svh = _f16(name, svh, "svh")
+    if suh.numel() < kdim or svh.numel() < n:
+        raise RuntimeError(f"sglang_exl3::{name}: suh needs {kdim} and svh {n} elements "
+                           f"(got {suh.numel()}, {svh.numel()})")
     tr = trellis.contiguous()
     y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    if m == 0:
+        return y
     lib = _lib.lib()
     with torch.cuda.device(x.device):
         need = int(lib.exl3_gemm_workspace_size(m, kdim, n, int(K)))
         ws = workspace(x.device, need) if need else None
         rc = fn(x2.data_ptr(), tr.data_ptr(), suh.data_ptr(), svh.data_ptr(), y.data_ptr(), m, kdim, n,
-                int(K), _lib.codebook_from_mcg(bool(mcg)), 0 if ws is None else ws.data_ptr(),
-                0 if ws is None else ws.numel(), _stream_ptr(x))
-    _lib.check(rc, name)
+                int(K), int(cb), 0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+                _stream_ptr(x))
+    check_ws(rc, name, ws)
     return y
 
 
 def exl3_gemv_impl(x, trellis, suh, svh, K, mcg, mmode=1):
     if mmode not in (0, 1):
         raise RuntimeError("sglang_exl3::exl3_gemv: mmode must be 0 or 1")
-    return _gemv_like("exl3_gemv", _lib.lib().exl3_gemv, x, trellis, suh, svh, K, mcg, max_rows=64)
+    return _gemv_like("exl3_gemv", _lib.lib().exl3_gemv, x, trellis, suh, svh, K,
+                      _lib.codebook_from_mcg(bool(mcg)), max_rows=64)
 
 
 def exl3_gemm_impl(x, trellis, suh, svh, K, mcg):
-    return _gemv_like("exl3_gemm", _lib.lib().exl3_gemm, x, trellis, suh, svh, K, mcg)
+    return _gemv_like("exl3_gemm", _lib.lib().exl3_gemm, x, trellis, suh, svh, K, _lib.codebook_from_mcg(bool(mcg)))
+
+
+def exl3_linear_impl(x, trellis, suh, svh, K, codebook):
+    """Dense EXL3 linear for any row count and any codebook id (0 = 3INST,
+    1 = MCG, 2 = mul1): the single-flag ops above cannot name 3INST, which
+    EXL3LinearMethod needs for packs without a codebook marker
+    (src/sglang_exl3/dense.py:151-157)."""
+    return _gemv_like("exl3_linear", _lib.lib().exl3_gemm, x, trellis, suh, svh, K, int(codebook))
 
 
 def p2b_gemv_batched_impl(x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices, K, mcg, mmode=1):
@@ -165,7 +208,7 @@ def p2b_gemv_batched_impl(x, trellis_ptrs, suh_ptrs, svh_ptrs, expert_indices, K
             suh_ptrs.contiguous().data_ptr(), svh_ptrs.contiguous().data_ptr(), ids.data_ptr(), e,
             out.data_ptr(), m, kdim, n, int(K), _lib.codebook_from_mcg(bool(mcg)),
             0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), _stream_ptr(x))
-    _lib.check(rc, name)
+    check_ws(rc, name, ws)
     return out
 
 
@@ -225,7 +268,7 @@ def p2b_fused_moe_impl(x, out, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, 
             x.data_ptr(), out.data_ptr(), *[t.data_ptr() for t in tabs], E, ids.data_ptr(), rw.data_ptr(),
             ids.numel(), hidden, inter, int(K_gate), int(K_up), int(K_down), _lib.codebook_from_mcg(bool(mcg)),
             _limit_arg(swiglu_limit), ws.data_ptr(), ws.numel(), _stream_ptr(x))
-    _lib.check(rc, name)
+    check_ws(rc, name, ws)
     return out
 
 
@@ -260,7 +303,7 @@ def exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_p
             xh.data_ptr(), ids.data_ptr(), w.data_ptr(), *[t.data_ptr() for t in tabs], E, out.data_ptr(), T, topk,
             hidden, int(intermediate_size), int(K_gate), int(K_up), int(K_down),
             _lib.codebook_from_mcg(bool(mcg)), lim, ws.data_ptr(), ws.numel(), _stream_ptr(x))
-    _lib.check(rc, name)
+    check_ws(rc, name, ws)
     return out
 
 
@@ -351,6 +394,16 @@ def register_custom_ops() -> bool:
     def _(x, trellis, suh, svh, K, mcg):
         out_dim = svh.size(0) if svh.ndim == 1 else trellis.size(1) * 16
         return torch.empty((x.shape[0], out_dim), dtype=x.dtype, device=x.device)
+
+    @torch.library.custom_op("sglang_exl3::exl3_linear", mutates_args=())
+    def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
+                    codebook: int) -> torch.Tensor:
+        return exl3_linear_impl(x, trellis, suh, svh, K, codebook)
+
+    @exl3_linear.register_fake
+    def _(x, trellis, suh, svh, K, codebook):
+        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        return torch.empty((rows, trellis.size(1) * 16), dtype=torch.float16, device=x.device)
 
     @torch.library.custom_op("sglang_exl3::p2b_gemv_batched", mutates_args=())
     def p2b_gemv_batched(x: torch.Tensor, trellis_ptrs: torch.Tensor, suh_ptrs: torch.Tensor,

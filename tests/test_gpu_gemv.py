@@ -269,3 +269,37 @@ def test_gemv_balanced_leaves_accumulators_zero():
         torch.cuda.synchronize()
         assert int(torch.count_nonzero(ws)) == 0
     check_close(y.float().cpu().numpy(), _oracle_ref(x, trellis, suh, svh, K, 1), "balanced ws")
+
+
+def test_workspace_growth_keeps_captured_graphs_valid():
+    """A graph captured with the stream's workspace stays correct after a larger
+    op grew that workspace (the old buffer is kept alive, not freed); growth
+    itself is refused during capture."""
+    k, n, K = 512, 1024, 4
+    tr, su, sv = make_weight(k, n, K, seed=71)
+    x = make_x(8, k, seed=72)
+    d = to_dev(x, tr, su, sv)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        torch.ops.sglang_exl3.exl3_gemv(*d, K, True, 1)  # sizes the stream's workspace
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            y = torch.ops.sglang_exl3.exl3_gemv(*d, K, True, 1)
+        # grow the workspace of the same stream well past its first size
+        kb, nb = 4096, 8192
+        trb, sub, svb = make_weight(kb, nb, 2, seed=73)
+        xb = make_x(64, kb, seed=74)
+        yb = torch.ops.sglang_exl3.exl3_gemv(*to_dev(xb, trb, sub, svb), 2, True, 1)
+        for _ in range(3):
+            g.replay()
+    torch.cuda.synchronize()
+    ref = oracle.matmul(x, oracle.dequant(tr, su, sv, K, 1, rtz=True))
+    check_close(y.float().cpu().numpy(), ref, "graph replay after workspace growth")
+    assert yb.shape == (64, nb)
+    # an op whose workspace would have to grow during capture is refused with a clear message
+    s2 = torch.cuda.Stream()
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="during HIP graph capture"):
+        with torch.cuda.stream(s2):
+            with torch.cuda.graph(g2, stream=s2):
+                torch.ops.sglang_exl3.exl3_gemv(*d, K, True, 1)

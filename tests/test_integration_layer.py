@@ -179,13 +179,24 @@ def test_map_topk_to_local():
 
 
 def test_tp_sharding_helpers():
-    t = torch.arange(4 * 6 * 2).reshape(4, 6, 2)
-    assert torch.equal(shard_exl3_col(t, "trellis", 1, 2), t[:, 3:6])
-    assert torch.equal(shard_exl3_row(t, "trellis", 1, 2), t[2:4])
-    assert torch.equal(shard_exl3_col(torch.arange(6), "svh", 0, 3), torch.arange(2))
-    assert torch.equal(shard_exl3_row(torch.arange(6), "suh", 2, 3), torch.arange(4, 6))
-    with pytest.raises(ValueError):
-        shard_exl3_col(t, "trellis", 0, 4)
+    t = torch.arange(4 * 16 * 8 * 2).reshape(4 * 8, 16, 2)  # [in tiles, out tiles, words]
+    assert torch.equal(shard_exl3_col(t, "trellis", 1, 2), t[:, 8:16])
+    assert torch.equal(shard_exl3_row(t, "trellis", 1, 2), t[16:32])
+    assert torch.equal(shard_exl3_row(t, "trellis", 3, 4), t[24:32])
+    assert torch.equal(shard_exl3_col(torch.arange(384), "svh", 1, 3), torch.arange(128, 256))
+    assert torch.equal(shard_exl3_row(torch.arange(384), "suh", 2, 3), torch.arange(256, 384))
+    # the shared vectors stay whole
+    assert torch.equal(shard_exl3_col(torch.arange(384), "suh", 1, 3), torch.arange(384))
+    assert torch.equal(shard_exl3_row(torch.arange(384), "svh", 1, 3), torch.arange(384))
+    with pytest.raises(ValueError, match="not divisible"):
+        shard_exl3_col(t, "trellis", 0, 3)
+    # inter 768 over tp=8 gives 96 columns (6 tiles): refused at load, not at apply
+    with pytest.raises(ValueError, match="multiple of 8"):
+        shard_exl3_col(torch.zeros(4, 48, 2), "trellis", 0, 8)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        shard_exl3_col(torch.zeros(768), "svh", 0, 8)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        shard_exl3_row(torch.zeros(768), "suh", 0, 8)
 
 
 def test_loader_packs_experts_and_markers():
