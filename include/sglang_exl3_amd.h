@@ -100,6 +100,24 @@ int exl3_gemv(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, co
               uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
               size_t workspace_bytes, void* stream);
 
+/* Bytes of the per-GPU scratch array behind exl3_gemv_noalloc. */
+#define EXL3_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* exl3_gemv without a workspace: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The split-k counters,
+ * accumulators and partial sums live in a file-scope device array of
+ * EXL3_NOALLOC_SCRATCH_BYTES per GPU (allocated with the library's code
+ * object, held until the process ends); shapes whose
+ * exl3_gemv_workspace_size(m, k, n, K, 1) exceeds it are refused with
+ * EXL3_ERR_UNSUPPORTED.  The first call on a GPU enqueues a clear of the
+ * array's zeroed regions on `stream`; every call leaves them zero again.
+ * All calls on one GPU share the array, so calls that overlap in time on
+ * one GPU (other streams, other threads) race; serialise them.
+ * Calls no hipMalloc / hipFree and allocates nothing. */
+int exl3_gemv_noalloc(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
+                      uint16_t* y, int m, int k, int n, int K, int codebook, void* stream);
+
 /* Same product for any number of rows m >= 1: up to 64 rows the GEMV kernel;
  * above, the input is rotated once and the MFMA GEMM (exl3_fat_gemm's
  * kernel) runs over it (workspace: exl3_gemm_workspace_size).

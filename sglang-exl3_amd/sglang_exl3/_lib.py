@@ -38,6 +38,7 @@ SIGNATURES = {
     "exl3_gemv_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
     "exl3_gemv_plan": (_I, [_I, _I, _I, _I, _I, _P]),
     "exl3_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    "exl3_gemv_noalloc": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "exl3_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_p2b_gemv_batched": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_hadamard_rows": (_I, [_P, _P, _P, _P, _F, _I, _I, _P]),

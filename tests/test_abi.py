@@ -142,3 +142,26 @@ def test_moe_rejects_bad_arguments_without_a_gpu():
     assert rc == _lib.EXL3_ERR_WORKSPACE
     rc = L.exl3_p2b_fused_moe(1, 1, *([1] * 9), 8, 1, 1, 4, 2048, 768, 3, 3, 9, 1, 0.0, None, 0, None)
     assert rc == _lib.EXL3_ERR_ARG and b"outside 1..8" in L.exl3_last_error()
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((None, None, None, None, None, 0, 4096, 4096, 4, 1, None), b"m=0"),
+    ((None, None, None, None, None, 65, 4096, 4096, 4, 1, None), b"m=65"),
+    ((None, None, None, None, None, 1, 4000, 4096, 4, 1, None), b"multiples of 128"),
+    ((None, None, None, None, None, 1, 4096, 4096, 0, 1, None), b"K=0"),
+    ((None, None, None, None, None, 1, 4096, 4096, 4, 7, None), b"codebook=7"),
+    ((None, None, None, None, None, 1, 4096, 4096, 4, 1, None), b"null pointer"),
+])
+def test_gemv_noalloc_rejects_bad_arguments_before_the_device(args, needle):
+    L = _lib.lib()
+    assert L.exl3_gemv_noalloc(*args) == _lib.EXL3_ERR_ARG
+    assert needle in L.exl3_last_error()
+
+
+def test_gemv_noalloc_refuses_shapes_beyond_its_scratch():
+    L = _lib.lib()
+    # 64 rows x 65536 columns need far more than the fixed 32 MiB (non-null dummy pointers: refused before use)
+    assert L.exl3_gemv_workspace_size(64, 4096, 65536, 4, 1) > (32 << 20)
+    rc = L.exl3_gemv_noalloc(16, 16, 16, 16, 16, 64, 4096, 65536, 4, 1, None)
+    assert rc == _lib.EXL3_ERR_UNSUPPORTED
+    assert b"above the fixed" in L.exl3_last_error()
