@@ -150,6 +150,30 @@ int exl3_fat_gemm_scatter(const uint16_t* a, const int16_t* trellis, float* out,
                           const int64_t* token_idx, const uint16_t* route_weight, int M, int k, int n, int K,
                           int codebook, void* stream);
 
+/* Scratch bytes exl3_gate_up_swiglu needs for m rows (zero-filled before its
+ * first use, left zeroed by every call, like the GEMV workspace). */
+size_t exl3_gate_up_workspace_size(int m, int k, int n, int K);
+
+/* Fused gate + up projection with the SwiGLU applied:
+ *   out[m][n] (f16) = fp16( silu(min(g, L)) * clamp(u, -L, L) ),
+ *   g = x . W_gate, u = x . W_up  (x: f16 [m][k]),
+ * where both weights share the input rotation `suh` (f16 [k]), as the
+ * reference's fused gate/up path rotates the input once with the gate's suh
+ * for both (src/sglang_exl3/exl3.py:1184-1206: exl3_fat_gemm over the
+ * concatenated packs, then clamp, sigmoid * gate * up and the fp16 copy in
+ * torch).  Trellis [k/16][n/16][16K] and svh f16 [n] per projection, one K
+ * and codebook.  L = swiglu_limit; 0 or inf: no clamp.  Up to 64 rows the
+ * gate/up GEMV kernel (g and u rounded to fp16 before the SwiGLU, as the
+ * reference's batched decode path returns them, exl3.py:1018-1034); above,
+ * the input is rotated once and the wide-tile MFMA kernel computes both
+ * projections of a column block in one workgroup and applies the SwiGLU in
+ * its epilogue (g and u in fp32).  Replaces the gate/up half of
+ * apply_exl3_batched_fat (src/sglang_exl3/exl3.py:1154-1206). */
+int exl3_gate_up_swiglu(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis,
+                        const uint16_t* gate_svh, const int16_t* up_trellis, const uint16_t* up_svh,
+                        uint16_t* out, int m, int k, int n, int K, int codebook, float swiglu_limit,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* For each active slot e < num_active: out[e] (f16 [m][n]) = x_e . W_{ids[e]}
  * where x_e = x (x_per_expert == 0, x is [m][k]) or x + e*m*k (x_per_expert
  * != 0, x is [num_active][m][k]); weight pointers come from int64 device

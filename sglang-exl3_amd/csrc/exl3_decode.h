@@ -117,6 +117,10 @@ __device__ __forceinline__ __half2 h2_rn(float a, float b) {
     return __floats2half2_rn(a, b);
 }
 
+// SiLU in fp32, g * sigmoid(g) = g / (1 + e^-g) (the reference's SwiGLU:
+// csrc/p2b_moe.cu:283-290, src/sglang_exl3/exl3.py:1199-1206).
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
 // +1.0f where bit J of lane is clear, -1.0f where it is set.
 template <int J>
 __device__ __forceinline__ float lane_sign(int lane) {

@@ -182,6 +182,74 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
     return launch_status("exl3_gemm convert launch");
 }
 
+// Gate/up SwiGLU on the MFMA kernels: the input is rotated once with the
+// shared suh into the scratch, then
+//   * up to 64 rows: the narrow kernel in gate/up mode (16- or 64-row tiles,
+//     k-splits toward ~4 workgroups per CU; partial tiles and one counter per
+//     (column block, row tile) in the scratch);
+//   * above: the wide-tile kernel in gate/up mode (one split).
+// Scratch: [counters][accumulators][xr fp16 m*k][partials, narrow only].
+struct GateUpFatPlan {
+    int mt, splits;
+};
+
+GateUpFatPlan plan_gate_up_fat(int m, int k, int n) {
+    if (m > 64) return GateUpFatPlan{FAT_MT_WIDE, 1};
+    GateUpFatPlan pl{m <= 16 ? 16 : 64, 1};
+    const int ksteps = k / 64;
+    const long long base = 2LL * (n / 128) * ((m + pl.mt - 1) / pl.mt);
+    while (base * pl.splits * 2 <= 1024 && pl.splits < 16 && ksteps % (2 * pl.splits) == 0 &&
+           (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+        pl.splits *= 2;
+    return pl;
+}
+
+size_t fat_gate_up_scratch_bytes(int m, int k, int n) {
+    const GateUpFatPlan pl = plan_gate_up_fat(m, k, n);
+    size_t b = kWsScratchOffset + fat_xr_bytes(m, k);
+    if (pl.mt != FAT_MT_WIDE) b += (size_t)2 * (n / 128) * pl.splits * (size_t)m * 128 * sizeof(float);
+    return b;
+}
+
+int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis, const uint16_t* gate_svh,
+                     const int16_t* up_trellis, const uint16_t* up_svh, uint16_t* out, int m, int k, int n, int K,
+                     int cb, float limit, void* ws, size_t ws_bytes, hipStream_t st) {
+    const GateUpFatPlan pl = plan_gate_up_fat(m, k, n);
+    const size_t need = fat_gate_up_scratch_bytes(m, k, n);
+    EXL3_REQUIRE_CODE(ws && ws_bytes >= need, EXL3_ERR_WORKSPACE,
+                      "exl3_gate_up_swiglu: %zu workspace bytes needed for m=%d, %zu given", need, m,
+                      ws ? ws_bytes : (size_t)0);
+    EXL3_REQUIRE(aligned(gate_trellis, 16) && aligned(up_trellis, 16) && aligned(gate_svh, 4) && aligned(up_svh, 4),
+                 "exl3_gate_up_swiglu: misaligned pointer");
+    const int mtiles = pl.mt == FAT_MT_WIDE ? 1 : (m + pl.mt - 1) / pl.mt;
+    EXL3_REQUIRE_CODE((size_t)(n / 128) * mtiles <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
+                      "exl3_gate_up_swiglu: %d column blocks exceed the workspace counters", n / 128);
+    char* w8 = reinterpret_cast<char*>(ws);
+    __half* xr = reinterpret_cast<__half*>(w8 + kWsScratchOffset);
+    const long long chunks = (long long)m * (k / 128);
+    rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x),
+                                                                      reinterpret_cast<const __half*>(suh), xr, chunks,
+                                                                      k);
+    int rc = launch_status("exl3_gate_up_swiglu rotate launch");
+    if (rc) return rc;
+    FatParams p{};
+    p.a = xr;
+    p.trellis = reinterpret_cast<const uint32_t*>(gate_trellis);
+    p.svh = reinterpret_cast<const __half*>(gate_svh);
+    p.trellis2 = reinterpret_cast<const uint32_t*>(up_trellis);
+    p.svh2 = reinterpret_cast<const __half*>(up_svh);
+    p.out16 = reinterpret_cast<__half*>(out);
+    p.M = m;
+    p.k = k;
+    p.n = n;
+    p.ksteps = k / 64 / pl.splits;
+    p.gu = 1;
+    p.limit = limit;
+    p.counters = reinterpret_cast<int*>(w8);
+    p.partials = reinterpret_cast<float*>(w8 + kWsScratchOffset + fat_xr_bytes(m, k));
+    return fat_launch(K, cb, pl.mt, p, pl.splits, st);
+}
+
 }  // namespace exl3
 
 using namespace exl3;

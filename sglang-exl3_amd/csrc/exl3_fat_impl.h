@@ -41,6 +41,19 @@ struct FatParams {
     int M, k, n;
     int ksteps;      // steps (4 k-slices) per k-split
     int accumulate;  // add atomically into out32 instead of storing
+    // Gate/up mode (fat_big_kernel<.., GU = true>): `trellis`/`svh` are the
+    // gate projection, `trellis2`/`svh2` the up projection, both n wide;
+    // out16[m][n] = fp16( silu(min(g, limit)) * clamp(u, -limit, limit) ).
+    // fat_gemm_kernel in gate/up mode: grid.x enumerates (column block,
+    // projection) pairs (even: gate, odd: up); each workgroup stores its fp32
+    // partial tile, and the last of the 2 S arrivals of a (column block, row
+    // tile) sums them, applies both output rotations and the SwiGLU.
+    int gu;
+    const uint32_t* trellis2;
+    const __half* svh2;
+    float limit;  // <= 0 or inf: no clamp
+    float* partials;  // [n/128][2][S][M][128] (narrow gate/up mode)
+    int* counters;    // [n/128][row tiles], zero between calls
 };
 
 template <int K>
@@ -61,7 +74,10 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
     static_assert(FAT_CH % D == 0, "the register slot of a step must be static inside a chunk");
     extern __shared__ __align__(16) unsigned char fat_smem[];
 
-    const int bx = blockIdx.x, sidx = blockIdx.z;
+    const int sidx = blockIdx.z;
+    // gate/up mode: blockIdx.x = 2 * column block + projection
+    const int bx = p.gu ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
+    const uint32_t* trel = (p.gu && (blockIdx.x & 1)) ? p.trellis2 : p.trellis;
     const int m0 = blockIdx.y * MT;
     const int rows = min(MT, p.M - m0);
     const int tid = threadIdx.x, cw = tid >> 6, lane = tid & 63;
@@ -70,7 +86,7 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
     const int nsteps = p.ksteps;
     const int kt0 = sidx * nsteps * 4;
     const int nt = bx * 8 + cw * 2 + (i >> 3);
-    const EXL3_GLOBAL uint32_t* tb = gptr(p.trellis) + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
+    const EXL3_GLOBAL uint32_t* tb = gptr(trel) + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
     const __half2 svv = ld_h2(gptr(p.svh) + bx * 128 + 2 * lane);  // epilogue scale, requested early
@@ -149,8 +165,50 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
                 if (row < rows) ct[row * 128 + col] = acc[rb][c][r];
             }
     __syncthreads();
-    const float sva = __low2float(svv), svb = __high2float(svv);
     const int c0 = bx * 128 + 2 * lane;
+    if (p.gu) {
+        // hand-off of the gate/up mode: partial tile out (device-coherent
+        // stores), one counter per (column block, row tile); the last arrival
+        // sums each row's splits in split order (deterministic)
+        const int S = gridDim.z, proj = blockIdx.x & 1;
+        const size_t rs = (size_t)p.M * 128;  // between splits
+        float* part = p.partials + ((size_t)(bx * 2 + proj) * S + sidx) * rs + (size_t)m0 * 128;
+        for (int idx = tid; idx < rows * 128; idx += FAT_THREADS) coherent_store(part + idx, ct[idx]);
+        wait_stores();
+        __syncthreads();
+        __shared__ int gu_last;
+        int* ctr = p.counters + (size_t)bx * gridDim.y + blockIdx.y;
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            gu_last = old == 2 * S - 1;
+        }
+        __syncthreads();
+        if (!gu_last) return;
+        if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float* pg = p.partials + (size_t)(bx * 2) * S * rs + (size_t)m0 * 128 + 2 * lane;
+        const float* pu = p.partials + (size_t)(bx * 2 + 1) * S * rs + (size_t)m0 * 128 + 2 * lane;
+        const __half2 svg = ld_h2(gptr(p.svh) + c0), svu = ld_h2(gptr(p.svh2) + c0);
+        const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
+        for (int row = cw; row < rows; row += FAT_THREADS / 64) {
+            float ga = sum_splits(pg + row * 128, rs, S), gb = sum_splits(pg + row * 128 + 1, rs, S);
+            float ua = sum_splits(pu + row * 128, rs, S), ub = sum_splits(pu + row * 128 + 1, rs, S);
+            fwht128_pair_fast(ga, gb, lane);
+            fwht128_pair_fast(ua, ub, lane);
+            ga = (ga * kHadNorm) * __low2float(svg);
+            gb = (gb * kHadNorm) * __high2float(svg);
+            ua = (ua * kHadNorm) * __low2float(svu);
+            ub = (ub * kHadNorm) * __high2float(svu);
+            if (clamp) {
+                ga = fminf(ga, p.limit);
+                gb = fminf(gb, p.limit);
+                ua = fminf(fmaxf(ua, -p.limit), p.limit);
+                ub = fminf(fmaxf(ub, -p.limit), p.limit);
+            }
+            st_h2(gptr(p.out16) + (size_t)(m0 + row) * p.n + c0, h2_rn(silu_f(ga) * ua, silu_f(gb) * ub));
+        }
+        return;
+    }
+    const float sva = __low2float(svv), svb = __high2float(svv);
     for (int row = cw; row < rows; row += FAT_THREADS / 64) {
         float va = ct[row * 128 + 2 * lane], vb = ct[row * 128 + 2 * lane + 1];
         fwht128_pair_fast(va, vb, lane);
@@ -257,7 +315,14 @@ __device__ __forceinline__ void nat_group(const uint32_t (&w)[K], int prev_addr,
     nat_column<K, CB, 1>(buf, mid, f[1]);
 }
 
-template <int K, int CB>
+// GU = true: gate/up mode.  Workgroup bx then covers column block bx of both
+// projections: its left 128 columns (column quarters 0, 1) decode the gate
+// trellis, its right 128 (quarters 2, 3) the up trellis, so the epilogue
+// holds the gate and up values of the same columns and applies the SwiGLU
+// in registers.  The reference's fused path concatenates the two packs per
+// call and combines them with separate torch kernels
+// (src/sglang_exl3/exl3.py:1184-1206).
+template <int K, int CB, bool GU>
 __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
     constexpr int RB = FB_ROWS / 2 / 16;  // row blocks per wave
     static_assert(FB_A_BYTES == 4 * 16 * FB_THREADS, "four 16-byte A chunks per thread and step");
@@ -274,8 +339,10 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
     const int nsteps = p.ksteps;  // even
     const int kt0 = sidx * nsteps * 4;
     // this wave decodes group rh of quarter cq: column tiles 4cq + 2rh + (i >> 3)
-    const int nt = bx * (FB_COLS / 16) + cq * 4 + rh * 2 + (i >> 3);
-    const EXL3_GLOBAL uint32_t* tb = gptr(p.trellis) + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
+    // (gate/up mode: quarters 0, 1 of the gate block bx, 2, 3 of the up block bx)
+    const int nt = GU ? bx * 8 + (cq & 1) * 4 + rh * 2 + (i >> 3) : bx * (FB_COLS / 16) + cq * 4 + rh * 2 + (i >> 3);
+    const uint32_t* trel = (GU && cq >= 2) ? p.trellis2 : p.trellis;
+    const EXL3_GLOBAL uint32_t* tb = gptr(trel) + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
 
@@ -413,6 +480,54 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
                         ct[row * FB_CTS + col] = acc[pass * 2 + rr][G][c][r];
                     }
         __syncthreads();
+        if constexpr (GU) {
+            // 8 rows per wave, gate and up of one 128-column block: lane l
+            // holds 16 consecutive columns (16 (l & 7) ..) of each, LDS row
+            // 8 wv + (l >> 3); output FWHT, norm and svh of both, then SwiGLU
+            static_assert(FB_PASS_ROWS / 8 == FB_THREADS / 64, "one row group per wave");
+            const int ctr = wv * 8 + (lane >> 3);
+            const int trow = (ctr >> 5) * 128 + pass * 32 + (ctr & 31);
+            const int col = (lane & 7) * 16;
+            float gv[16], uv[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 a = *reinterpret_cast<const float4*>(ct + ctr * FB_CTS + col + 4 * q4);
+                const float4 b = *reinterpret_cast<const float4*>(ct + ctr * FB_CTS + 128 + col + 4 * q4);
+                gv[4 * q4] = a.x; gv[4 * q4 + 1] = a.y; gv[4 * q4 + 2] = a.z; gv[4 * q4 + 3] = a.w;
+                uv[4 * q4] = b.x; uv[4 * q4 + 1] = b.y; uv[4 * q4 + 2] = b.z; uv[4 * q4 + 3] = b.w;
+            }
+            fwht128_x16(gv, lane);
+            fwht128_x16(uv, lane);
+            const int c0 = bx * 128 + col;
+            const EXL3_GLOBAL uint32_t* sgp = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh) + c0);
+            const EXL3_GLOBAL uint32_t* sup = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh2) + c0);
+            const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
+            uint32_t ow[8];
+#pragma unroll
+            for (int e2 = 0; e2 < 8; ++e2) {
+                const uint32_t sgw = sgp[e2], suw = sup[e2];
+                float r[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int e = 2 * e2 + h;
+                    float gg = (gv[e] * kHadNorm) * __half2float(__ushort_as_half((unsigned short)(sgw >> (16 * h))));
+                    float uu = (uv[e] * kHadNorm) * __half2float(__ushort_as_half((unsigned short)(suw >> (16 * h))));
+                    if (clamp) {
+                        gg = fminf(gg, p.limit);
+                        uu = fminf(fmaxf(uu, -p.limit), p.limit);
+                    }
+                    r[h] = silu_f(gg) * uu;
+                }
+                const __half2 o = h2_rn(r[0], r[1]);
+                ow[e2] = *reinterpret_cast<const uint32_t*>(&o);
+            }
+            if (trow < rows) {
+                EXL3_GLOBAL uint32_t* o = reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(p.out16) + (size_t)(m0 + trow) * p.n + c0);
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) o[e2] = ow[e2];
+            }
+            continue;
+        }
         // 8 rows x one 128-block per wave at a time: lane l holds 16 consecutive
         // columns (16 (l & 7) ..) of LDS row 8 rg + (l >> 3)
 #pragma unroll
@@ -490,20 +605,21 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
 template <int K>
 int fat_launch_k(int cb, int mt, const FatParams& p, int splits, hipStream_t st) {
     if (mt == FAT_MT_WIDE) {
-        dim3 grid(p.n / FB_COLS, (p.M + FB_ROWS - 1) / FB_ROWS, splits);
+        dim3 grid(p.gu ? p.n / 128 : p.n / FB_COLS, (p.M + FB_ROWS - 1) / FB_ROWS, splits);
         const size_t smem = fat_big_smem_bytes();
-#define EXL3_FATB(CBV)                                                                                 \
-    if (cb == CBV) {                                                                                   \
-        const void* fn = reinterpret_cast<const void*>(&fat_big_kernel<K, CBV>);                       \
+#define EXL3_FATB(CBV, GUV)                                                                            \
+    if (cb == CBV && (p.gu != 0) == GUV) {                                                             \
+        const void* fn = reinterpret_cast<const void*>(&fat_big_kernel<K, CBV, GUV>);                  \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 fat gemm (wide tiles)");                     \
         if (lrc) return lrc;                                                                           \
-        fat_big_kernel<K, CBV><<<grid, FB_THREADS, smem, st>>>(p);                                     \
+        fat_big_kernel<K, CBV, GUV><<<grid, FB_THREADS, smem, st>>>(p);                                \
         return launch_status("exl3 fat gemm launch");                                                  \
     }
-        EXL3_FATB(0) EXL3_FATB(1) EXL3_FATB(2)
+        EXL3_FATB(0, false) EXL3_FATB(1, false) EXL3_FATB(2, false)
+        EXL3_FATB(0, true) EXL3_FATB(1, true) EXL3_FATB(2, true)
 #undef EXL3_FATB
     }
-    dim3 grid(p.n / 128, (p.M + mt - 1) / mt, splits);
+    dim3 grid((p.gu ? 2 : 1) * (p.n / 128), (p.M + mt - 1) / mt, splits);
     const size_t smem = fat_smem_bytes(mt);
 #define EXL3_FAT(CBV, MTV)                                                                             \
     if (cb == CBV && mt == MTV) {                                                                      \

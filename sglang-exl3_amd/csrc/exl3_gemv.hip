@@ -235,10 +235,95 @@ GemvParams base_params(const uint16_t* x, const int16_t* trellis, const uint16_t
     return p;
 }
 
+// --------------------------------------------------- dense gate + up (m <= 64)
+
+// Gate and up as the two "experts" of one k-split GEMV launch; the last of a
+// column block's 2 S workgroups applies the SwiGLU.  Scratch: counters (one
+// per column block) and the partials of both projections, always (the
+// hand-off needs them even when the plan has a single split).
+GemvPlan plan_gate_up(int m, int k, int n, int K) { return plan_gemv(m, k, n, K, 2); }
+
+size_t gate_up_gemv_bytes(int m, int k, int n, int K) {
+    const GemvPlan pl = plan_gate_up(m, k, n, K);
+    return kWsScratchOffset + (size_t)2 * (n / 128) * pl.splits * (size_t)m * 128 * sizeof(float);
+}
+
+int run_gate_up_gemv(const uint16_t* x, const uint16_t* suh, const int16_t* gt, const uint16_t* gsv,
+                     const int16_t* ut, const uint16_t* usv, uint16_t* out, int m, int k, int n, int K, int cb,
+                     float limit, void* ws, size_t ws_bytes, hipStream_t st) {
+    const GemvPlan pl = plan_gate_up(m, k, n, K);
+    const size_t need = gate_up_gemv_bytes(m, k, n, K);
+    EXL3_REQUIRE_CODE(ws && ws_bytes >= need, EXL3_ERR_WORKSPACE,
+                      "exl3_gate_up_swiglu: workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+    EXL3_REQUIRE_CODE((size_t)(n / 128) <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
+                      "exl3_gate_up_swiglu: %d column blocks exceed the workspace counters", n / 128);
+    EXL3_REQUIRE(aligned(gt, 16) && aligned(ut, 16) && aligned(gsv, 4) && aligned(usv, 4),
+                 "exl3_gate_up_swiglu: misaligned pointer");
+    GemvParams p = base_params(x, gt, suh, gsv, out, m, k, n);
+    p.gu = 1;
+    p.trellis2 = reinterpret_cast<const uint32_t*>(ut);
+    p.suh2 = reinterpret_cast<const __half*>(suh);
+    p.svh2 = reinterpret_cast<const __half*>(usv);
+    p.limit = limit;
+    p.nsteps = pl.nsteps;
+    p.kw = pl.kw;
+    p.splits = pl.splits;
+    p.counters = reinterpret_cast<int*>(ws);
+    p.partials = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsScratchOffset);
+    return gemv_launch(K, cb, pl.mb, p, 2, st);
+}
+
 }  // namespace
+
+// Rows up to which exl3_gate_up_swiglu runs the GEMV kernel; above, the input
+// is rotated once and the MFMA kernels run in gate/up mode.  Graph-timed on
+// config 3 (k = 4096, n = 2 x 14336, K = 3): m = 1 / 2 / 4: GEMV 26.7 / 28.7 /
+// 32.7 us against 33.5 / 34.2 / 34.4 us; m = 8 / 16 / 64: 41.5 / 58.8 / 298 us
+// against 37.6 / 44.3 / 90.8 us (the GEMV workgroups each re-rotate all m
+// input rows of their k range).
+constexpr int kGateUpMaxGemvRows = 4;
+
+size_t fat_gate_up_scratch_bytes(int m, int k, int n);
+int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis, const uint16_t* gate_svh,
+                     const int16_t* up_trellis, const uint16_t* up_svh, uint16_t* out, int m, int k, int n, int K,
+                     int cb, float limit, void* ws, size_t ws_bytes, hipStream_t st);
+
 }  // namespace exl3
 
 using namespace exl3;
+
+extern "C" size_t exl3_gate_up_workspace_size(int m, int k, int n, int K) {
+    if (m < 1 || k < 128 || n < 128 || k % 128 || n % 128 || K < 1 || K > 8) return 0;
+    const int gemv_rows = env_int("EXL3_GATE_UP_GEMV_ROWS", kGateUpMaxGemvRows);
+    size_t need = m > gemv_rows ? fat_gate_up_scratch_bytes(m, k, n) : gate_up_gemv_bytes(m, k, n, K);
+    if (m <= 64) {  // room for both paths (EXL3_GATE_UP_GEMV_ROWS moves the switch point)
+        const size_t c = fat_gate_up_scratch_bytes(m, k, n), d = gate_up_gemv_bytes(m, k, n, K);
+        need = need > c ? need : c;
+        need = need > d ? need : d;
+    }
+    return need;
+}
+
+extern "C" int exl3_gate_up_swiglu(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis,
+                                   const uint16_t* gate_svh, const int16_t* up_trellis, const uint16_t* up_svh,
+                                   uint16_t* out, int m, int k, int n, int K, int codebook, float swiglu_limit,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    EXL3_REQUIRE(m >= 1, "exl3_gate_up_swiglu: m=%d must be >= 1", m);
+    int rc = check_common("exl3_gate_up_swiglu", m, k, n, K, codebook);
+    if (rc) return rc;
+    EXL3_REQUIRE(x && suh && gate_trellis && gate_svh && up_trellis && up_svh && out,
+                 "exl3_gate_up_swiglu: null pointer");
+    EXL3_REQUIRE(aligned(x, 4) && aligned(out, 4) && aligned(suh, 4), "exl3_gate_up_swiglu: misaligned pointer");
+    EXL3_REQUIRE(!(swiglu_limit < 0.0f) && swiglu_limit == swiglu_limit,
+                 "exl3_gate_up_swiglu: swiglu_limit must be >= 0 (0 or inf: no clamp)");
+    hipStream_t st = as_stream(stream);
+    if (m > env_int("EXL3_GATE_UP_GEMV_ROWS", kGateUpMaxGemvRows))
+        return fat_gate_up_rows(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, out, m, k, n, K, codebook,
+                                swiglu_limit, workspace, workspace_bytes, st);
+    return run_gate_up_gemv(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, out, m, k, n, K, codebook,
+                            swiglu_limit, workspace, workspace_bytes, st);
+}
 
 extern "C" size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int experts) {
     if (m < 1 || k < 128 || n < 128 || experts < 1) return 0;

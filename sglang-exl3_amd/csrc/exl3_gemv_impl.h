@@ -49,6 +49,15 @@ struct GemvParams {
     int nsteps;  // steps (4 k-slices each) per wave
     int kw;      // waves along k inside a workgroup (1 or 2)
     int splits;  // S: workgroups along k
+    // Gate/up mode (two "experts" on grid.z: 0 = gate with trellis/suh/svh,
+    // 1 = up with trellis2/suh2/svh2): the 2 S workgroups of a column block
+    // share one counter, and the last of them writes
+    // y[row][col] = fp16( silu(min(g, limit)) * clamp(u, -limit, limit) ).
+    int gu;
+    const uint32_t* trellis2;
+    const __half* suh2;
+    const __half* svh2;
+    float limit;
 };
 
 // Steps of weight words a wave keeps in flight.  Measured on MI355X (config 2,
@@ -297,6 +306,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         trellis = reinterpret_cast<const uint32_t*>(gptr(p.t_tab)[id]);
         suh = reinterpret_cast<const __half*>(gptr(p.su_tab)[id]);
         svh = reinterpret_cast<const __half*>(gptr(p.sv_tab)[id]);
+    } else if (p.gu && e) {
+        trellis = p.trellis2;
+        suh = p.suh2;
+        svh = p.svh2;
     } else {
         trellis = p.trellis;
         suh = p.suh;
@@ -425,19 +438,54 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     // hand-off needs only "my stores completed" before the counter increment;
     // no L2 write-back or invalidate.
     const int nblk_n = n >> 7;
-    if (p.splits > 1) {
+    if (p.splits > 1 || p.gu) {
         const size_t cblk = (size_t)e * nblk_n + bx;
         float* part = p.partials + (cblk * p.splits + sidx) * (size_t)m * 128;
         for (int idx = tid; idx < m * 128; idx += nthreads) coherent_store(part + idx, ybuf[idx]);
         wait_stores();
         __syncthreads();
         __shared__ int is_last;
+        // gate/up mode: one counter per column block for both projections
+        const size_t ctr = p.gu ? (size_t)bx : cblk;
+        const int arrivals = p.gu ? 2 * p.splits : p.splits;
         if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(p.counters + cblk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            is_last = (old == p.splits - 1);
+            const int old = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            is_last = (old == arrivals - 1);
         }
         __syncthreads();
         if (!is_last) return;
+        if (p.gu) {
+            // gate and up of each row: split sums (one round trip each), output
+            // rotation, norm and svh of both, then the SwiGLU
+            if (tid == 0) __hip_atomic_store(p.counters + ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const size_t rstride = (size_t)m * 128;
+            const float* pg = p.partials + (size_t)bx * p.splits * rstride;
+            const float* pu = p.partials + (size_t)(nblk_n + bx) * p.splits * rstride;
+            const int cc = bx * 128 + 2 * lane;
+            const __half2 svg = ld_h2(gptr(p.svh) + cc), svu = ld_h2(gptr(p.svh2) + cc);
+            const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
+            EXL3_GLOBAL __half* yg = gptr(p.y);
+            for (int row = wave; row < m; row += nwaves) {
+                float ga = sum_splits(pg + row * 128 + 2 * lane, rstride, p.splits);
+                float gb = sum_splits(pg + row * 128 + 2 * lane + 1, rstride, p.splits);
+                float ua = sum_splits(pu + row * 128 + 2 * lane, rstride, p.splits);
+                float ub = sum_splits(pu + row * 128 + 2 * lane + 1, rstride, p.splits);
+                fwht128_pair_fast(ga, gb, lane);
+                fwht128_pair_fast(ua, ub, lane);
+                ga = ga * kHadNorm * __low2float(svg);
+                gb = gb * kHadNorm * __high2float(svg);
+                ua = ua * kHadNorm * __low2float(svu);
+                ub = ub * kHadNorm * __high2float(svu);
+                if (clamp) {
+                    ga = fminf(ga, p.limit);
+                    gb = fminf(gb, p.limit);
+                    ua = fminf(fmaxf(ua, -p.limit), p.limit);
+                    ub = fminf(fmaxf(ub, -p.limit), p.limit);
+                }
+                st_h2(yg + (size_t)row * n + cc, h2_rn(silu_f(ga) * ua, silu_f(gb) * ub));
+            }
+            return;
+        }
         const float* base = p.partials + cblk * p.splits * (size_t)m * 128;
         for (int idx = tid; idx < m * 128; idx += nthreads) ybuf[idx] = sum_splits(base + idx, (size_t)m * 128, p.splits);
         if (tid == 0) __hip_atomic_store(p.counters + cblk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

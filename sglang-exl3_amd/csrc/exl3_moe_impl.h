@@ -118,8 +118,6 @@ inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
 
 // ------------------------------------------------------------ expert GEMVs
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
-
 // Wave-uniform values read from memory by vector loads, moved to scalar
 // registers (they would otherwise occupy a VGPR per lane).
 __device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }

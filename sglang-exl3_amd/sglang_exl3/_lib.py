@@ -45,6 +45,8 @@ SIGNATURES = {
     "exl3_gemm_workspace_size": (_SZ, [_I, _I, _I, _I]),
     "exl3_fat_gemm": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "exl3_fat_gemm_scatter": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "exl3_gate_up_workspace_size": (_SZ, [_I, _I, _I, _I]),
+    "exl3_gate_up_swiglu": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _SZ, _P]),
     "exl3_moe_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
     "exl3_moe_plan": (_I, [_I, _I, _I, _I, _I, _P]),
     "exl3_moe_layer": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I,

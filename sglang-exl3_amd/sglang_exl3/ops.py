@@ -307,6 +307,42 @@ def exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_p
     return out
 
 
+def exl3_gate_up_swiglu_impl(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, K, codebook, swiglu_limit=0.0):
+    """fp16 [rows, n] = silu(min(x @ W_gate, L)) * clamp(x @ W_up, -L, L) for x [..., k], both
+    projections sharing the input rotation suh (the reference's fused gate/up path rotates once
+    with the gate's suh: src/sglang_exl3/exl3.py:1184-1206)."""
+    name = "exl3_gate_up_swiglu"
+    _require_device(name, x, suh, gate_trellis, gate_svh, up_trellis, up_svh)
+    _check_trellis(name, gate_trellis, K)
+    _check_trellis(name, up_trellis, K)
+    if tuple(gate_trellis.shape) != tuple(up_trellis.shape):
+        raise RuntimeError(f"sglang_exl3::{name}: gate and up trellis shapes differ")
+    kdim = int(x.shape[-1])
+    m = x.numel() // kdim if kdim else 0
+    if kdim != int(gate_trellis.shape[0]) * 16:
+        raise RuntimeError(f"sglang_exl3::{name}: x feature dimension does not match trellis")
+    if int(codebook) not in (_lib.CB_3INST, _lib.CB_MCG, _lib.CB_MUL1):
+        raise RuntimeError(f"sglang_exl3::{name}: codebook id {codebook} outside 0..2")
+    n = int(gate_trellis.shape[1]) * 16
+    x2 = _f16(name, x, "x").reshape(m, kdim)
+    suh, gsv, usv = (_f16(name, t, w) for t, w in ((suh, "suh"), (gate_svh, "gate_svh"), (up_svh, "up_svh")))
+    if suh.numel() < kdim or gsv.numel() < n or usv.numel() < n:
+        raise RuntimeError(f"sglang_exl3::{name}: suh needs {kdim}, svh {n} elements")
+    gt, ut = gate_trellis.contiguous(), up_trellis.contiguous()
+    out = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    if m == 0:
+        return out
+    lib = _lib.lib()
+    with torch.cuda.device(x.device):
+        need = int(lib.exl3_gate_up_workspace_size(m, kdim, n, int(K)))
+        ws = workspace(x.device, need)
+        rc = lib.exl3_gate_up_swiglu(x2.data_ptr(), suh.data_ptr(), gt.data_ptr(), gsv.data_ptr(), ut.data_ptr(),
+                                     usv.data_ptr(), out.data_ptr(), m, kdim, n, int(K), int(codebook),
+                                     _limit_arg(swiglu_limit), ws.data_ptr(), ws.numel(), _stream_ptr(x))
+    check_ws(rc, name, ws)
+    return out
+
+
 def _fat_common(name, a, packed, out, svh, K):
     _require_device(name, a, packed, out, svh)
     if a.dtype != torch.float16 or a.dim() != 2 or not a.is_contiguous():
@@ -449,6 +485,18 @@ def register_custom_ops() -> bool:
     @exl3_moe_layer.register_fake
     def _(x, topk_ids, topk_weights, *rest):
         return torch.empty((x.shape[0], x.shape[1]), dtype=torch.float16, device=x.device)
+
+    @torch.library.custom_op("sglang_exl3::exl3_gate_up_swiglu", mutates_args=())
+    def exl3_gate_up_swiglu(x: torch.Tensor, suh: torch.Tensor, gate_trellis: torch.Tensor, gate_svh: torch.Tensor,
+                            up_trellis: torch.Tensor, up_svh: torch.Tensor, K: int, codebook: int,
+                            swiglu_limit: float = 0.0) -> torch.Tensor:
+        return exl3_gate_up_swiglu_impl(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, K, codebook,
+                                        swiglu_limit)
+
+    @exl3_gate_up_swiglu.register_fake
+    def _(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, K, codebook, swiglu_limit=0.0):
+        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        return torch.empty((rows, gate_trellis.size(1) * 16), dtype=torch.float16, device=x.device)
 
     @torch.library.custom_op("sglang_exl3::exl3_fat_gemm", mutates_args=("out",))
     def exl3_fat_gemm(a: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, svh: torch.Tensor, K: int,

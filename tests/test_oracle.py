@@ -216,13 +216,70 @@ def test_cpu_gemv_is_dequant_then_fp32_product():
     assert np.allclose(y, x.astype(np.float64) @ W, rtol=1e-4, atol=1e-3)
 
 
-def test_swiglu_matches_formula():
-    g = np.array([-3.0, -0.5, 0.0, 0.7, 4.0], dtype=np.float32)
-    u = np.array([1.0, -2.0, 3.0, 0.5, -9.0], dtype=np.float32)
-    want = g / (1 + np.exp(-g)) * u
-    assert np.allclose(oracle.swiglu(g, u, float("inf")), want, rtol=1e-6)
-    L = 1.0
-    wl = np.minimum(g, L) / (1 + np.exp(-np.minimum(g, L))) * np.clip(u, -L, L)
-    assert np.allclose(oracle.swiglu(g, u, L), wl, rtol=1e-6)
-    for gi, ui in zip(g, u):
-        assert oracle.lib().orc_swiglu(float(gi), float(ui), 0.0) == pytest.approx(float(gi / (1 + np.exp(-gi)) * ui), rel=1e-6)
+def test_swiglu_matches_torch_silu():
+    """oracle.swiglu against torch's own SiLU (an independent implementation of
+    silu(min(g, L)) * clamp(u, -L, L), src/sglang_exl3/exl3.py:572), on values
+    from the saturated tails through zero; and the C restatement agrees too."""
+    import torch
+
+    rng = np.random.default_rng(12)
+    g = np.concatenate([rng.standard_normal(4000) * 6, [-80.0, -20.0, -1e-3, 0.0, 1e-3, 20.0, 80.0]]).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32) * 3
+    for L in (float("inf"), 0.0, 1.0, 4.5):
+        gt, ut = torch.from_numpy(g.astype(np.float64)), torch.from_numpy(u.astype(np.float64))
+        if L > 0 and np.isfinite(L):
+            gt, ut = gt.clamp(max=L), ut.clamp(min=-L, max=L)
+        want = (torch.nn.functional.silu(gt) * ut).numpy()
+        got = oracle.swiglu(g, u, L)
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-30), f"limit {L}"
+    for gi, ui in zip(g[::400], u[::400]):
+        want = float(torch.nn.functional.silu(torch.tensor(float(gi), dtype=torch.float64)) * float(ui))
+        assert oracle.lib().orc_swiglu(float(gi), float(ui), 0.0) == pytest.approx(want, rel=2e-6, abs=1e-30)
+
+
+def _tiny_experts(E, hidden, inter, K, seed):
+    out = []
+    for e in range(E):
+        spec = {}
+        for j, (proj, k, n) in enumerate((("gate", hidden, inter), ("up", hidden, inter), ("down", inter, hidden))):
+            r = np.random.default_rng(seed + 3 * e + j)
+            tr = r.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int64).astype(np.int16)
+            su = np.where(r.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+            sv = (np.where(r.random(n) < 0.5, -1.0, 1.0) * (4.0 / np.sqrt(k))).astype(np.float16)
+            spec[proj] = (tr, su, sv, K, 1)
+        out.append(spec)
+    return out
+
+
+def test_moe_ref_reduces_to_composed_linears():
+    """Top-1 routing with weight 1 is down(swiglu(gate x, up x)) of that expert,
+    built from linear_ref; invalid ids contribute nothing."""
+    E, H, I, K = 3, 128, 128, 2
+    experts = _tiny_experts(E, H, I, K, seed=5)
+    x = np.random.default_rng(6).standard_normal((4, H)).astype(np.float16)
+    ids = np.array([[2], [0], [1], [-1]], dtype=np.int32)
+    w = np.ones((4, 1), dtype=np.float32)
+    got = oracle.moe_ref(x, ids, w, experts)
+    for t in range(3):
+        ex = experts[int(ids[t, 0])]
+        g = oracle.linear_ref(x[t:t + 1], *ex["gate"])
+        u = oracle.linear_ref(x[t:t + 1], *ex["up"])
+        act = oracle.swiglu(g, u, float("inf")).astype(np.float16)
+        want = oracle.linear_ref(act, *ex["down"])
+        assert np.array_equal(got[t], want[0])
+    assert not got[3].any()
+
+
+def test_moe_ref_is_linear_in_the_routing_weights():
+    """Doubling every routing weight doubles the output; two slots add up to the
+    sum of the one-slot outputs."""
+    E, H, I, K = 4, 128, 128, 3
+    experts = _tiny_experts(E, H, I, K, seed=9)
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((5, H)).astype(np.float16)
+    ids = np.stack([rng.choice(E, 2, replace=False) for _ in range(5)]).astype(np.int32)
+    w = rng.random((5, 2)).astype(np.float32)
+    base = oracle.moe_ref(x, ids, w, experts)
+    assert np.allclose(oracle.moe_ref(x, ids, 2 * w, experts), 2 * base, rtol=1e-6, atol=1e-6)
+    one = oracle.moe_ref(x, ids[:, :1], w[:, :1], experts) + oracle.moe_ref(x, ids[:, 1:], w[:, 1:], experts)
+    assert np.allclose(base, one, rtol=1e-5, atol=1e-5)
