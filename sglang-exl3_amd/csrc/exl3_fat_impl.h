@@ -30,6 +30,15 @@ constexpr int FAT_THREADS = 256;  // 4 waves x 32 output columns
 constexpr int FAT_CH = 4;         // steps per staged A chunk (256 k)
 constexpr int FAT_ROWB = FAT_CH * 4 * 2 * 16 + 16;  // bytes per staged A row (+16: bank spread)
 
+// A run of rows of one expert in compact (expert-sorted) order: one row tile
+// of the grouped mode, written by the MoE prefill routing kernel.
+struct alignas(16) FatTile {
+    int e;      // expert id
+    int crow0;  // first compact row
+    int nrows;  // 1..MT
+    int pad;
+};
+
 struct FatParams {
     const __half* a;          // [M][k] rotated activations
     const uint32_t* trellis;  // [k/16][n/16][16K] as words
@@ -54,6 +63,21 @@ struct FatParams {
     float limit;  // <= 0 or inf: no clamp
     float* partials;  // [n/128][2][S][M][128] (narrow gate/up mode)
     int* counters;    // [n/128][row tiles], zero between calls
+    // Grouped mode of fat_gemm_kernel (MoE prefill), gmode != 0: blockIdx.y
+    // indexes `tiles` (tiles at or past *ntiles exit at once, so the grid is
+    // static), `a` holds the rows in compact order, and the weights are the
+    // tile's expert's entries of the nine per-expert tables (gate, up, down x
+    // trellis, suh, svh).  One k-split.
+    //   gmode 1 (gate): g32[crow][n] = fp32 gate output;
+    //   gmode 2 (up):   out16[crow][n] = fp16(H(fp16(silu(min(g, L)) * clamp(u, -L, L)) (.) suh_down) / sqrt(128)),
+    //                   the activation already rotated for the down projection;
+    //   gmode 3 (down): out16[rows_map[crow]][n] = fp16 down output, by (token, slot) entry.
+    int gmode;
+    const FatTile* tiles;
+    const int* ntiles;
+    const int64_t* tabs[9];
+    float* g32;
+    const int* rows_map;
 };
 
 template <int K>
@@ -78,8 +102,21 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
     // gate/up mode: blockIdx.x = 2 * column block + projection
     const int bx = p.gu ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
     const uint32_t* trel = (p.gu && (blockIdx.x & 1)) ? p.trellis2 : p.trellis;
-    const int m0 = blockIdx.y * MT;
-    const int rows = min(MT, p.M - m0);
+    const __half* svh_p = p.svh;
+    const __half* dsuh = nullptr;  // grouped up pass: the down projection's suh
+    int m0 = blockIdx.y * MT;
+    int rows = min(MT, p.M - m0);
+    if (p.gmode) {
+        if ((int)blockIdx.y >= __builtin_amdgcn_readfirstlane(*gptr(p.ntiles))) return;
+        const EXL3_GLOBAL FatTile* tl = gptr(p.tiles) + blockIdx.y;
+        const int e = __builtin_amdgcn_readfirstlane(tl->e);
+        m0 = __builtin_amdgcn_readfirstlane(tl->crow0);
+        rows = __builtin_amdgcn_readfirstlane(tl->nrows);
+        const int pb = p.gmode == 1 ? 0 : (p.gmode == 2 ? 3 : 6);
+        trel = reinterpret_cast<const uint32_t*>(gptr(p.tabs[pb])[e]);
+        svh_p = reinterpret_cast<const __half*>(gptr(p.tabs[pb + 2])[e]);
+        if (p.gmode == 2) dsuh = reinterpret_cast<const __half*>(gptr(p.tabs[7])[e]);
+    }
     const int tid = threadIdx.x, cw = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
     const int ntiles = p.n >> 4;
@@ -89,7 +126,7 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
     const EXL3_GLOBAL uint32_t* tb = gptr(trel) + ((size_t)(kt0 + g) * ntiles + nt) * (8 * K) + K * q;
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const int prev_addr = ((lane & ~7) | ((lane + 7) & 7)) << 2;
-    const __half2 svv = ld_h2(gptr(p.svh) + bx * 128 + 2 * lane);  // epilogue scale, requested early
+    const __half2 svv = ld_h2(gptr(svh_p) + bx * 128 + 2 * lane);  // epilogue scale, requested early
 
     float4_t acc[RB][2];
 #pragma unroll
@@ -166,6 +203,43 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
             }
     __syncthreads();
     const int c0 = bx * 128 + 2 * lane;
+    if (p.gmode) {
+        const float sva = __low2float(svv), svb = __high2float(svv);
+        const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
+        __half2 ds = __half2{};
+        if (p.gmode == 2) ds = ld_h2(gptr(dsuh) + c0);
+        for (int row = cw; row < rows; row += FAT_THREADS / 64) {
+            float va = ct[row * 128 + 2 * lane], vb = ct[row * 128 + 2 * lane + 1];
+            fwht128_pair_fast(va, vb, lane);
+            va = (va * kHadNorm) * sva;
+            vb = (vb * kHadNorm) * svb;
+            const size_t crow = (size_t)(m0 + row);
+            if (p.gmode == 1) {
+                const float2 v2 = make_float2(va, vb);
+                *reinterpret_cast<EXL3_GLOBAL unsigned long long*>(gptr(p.g32) + crow * p.n + c0) =
+                    *reinterpret_cast<const unsigned long long*>(&v2);
+            } else if (p.gmode == 2) {
+                const unsigned long long gw =
+                    *reinterpret_cast<const EXL3_GLOBAL unsigned long long*>(gptr(p.g32) + crow * p.n + c0);
+                float ga = __uint_as_float((uint32_t)gw), gb = __uint_as_float((uint32_t)(gw >> 32));
+                if (clamp) {
+                    ga = fminf(ga, p.limit);
+                    gb = fminf(gb, p.limit);
+                    va = fminf(fmaxf(va, -p.limit), p.limit);
+                    vb = fminf(fmaxf(vb, -p.limit), p.limit);
+                }
+                // the activation in fp16, then the down projection's input rotation of this 128-wide chunk
+                const __half2 pr = __hmul2(h2_rn(silu_f(ga) * va, silu_f(gb) * vb), ds);
+                float da = __low2float(pr), db = __high2float(pr);
+                fwht128_pair_fast(da, db, lane);
+                st_h2(gptr(p.out16) + crow * p.n + c0, h2_rn(da * kHadNorm, db * kHadNorm));
+            } else {
+                const int entry = gptr(p.rows_map)[crow];
+                st_h2(gptr(p.out16) + (size_t)entry * p.n + c0, h2_rn(va, vb));
+            }
+        }
+        return;
+    }
     if (p.gu) {
         // hand-off of the gate/up mode: partial tile out (device-coherent
         // stores), one counter per (column block, row tile); the last arrival

@@ -5,6 +5,7 @@
 
 #include <mutex>
 
+#include "exl3_fat_impl.h"
 #include "exl3_moe_impl.h"
 
 namespace exl3 {
@@ -411,22 +412,11 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     return L;
 }
 
-int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* weights, int weights_f16,
-            const MoeTables& tb, int E, uint16_t* out, int tokens, int topk, int hidden, int inter, int KG,
-            int KU, int KD, int cb, float limit, void* ws, size_t ws_bytes, hipStream_t st) {
-    EXL3_REQUIRE(tokens >= 1 && topk >= 1, "%s: tokens=%d topk=%d must be >= 1", fn, tokens, topk);
-    EXL3_REQUIRE(E >= 1 && E <= kMoeMaxExperts, "%s: num_experts=%d outside 1..%d", fn, E, kMoeMaxExperts);
+int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const void* weights, int weights_f16,
+                   const MoeTables& tb, int E, uint16_t* out, int tokens, int topk, int hidden, int inter, int KG,
+                   int KU, int KD, int cb, float limit, void* ws, size_t ws_bytes, hipStream_t st) {
     EXL3_REQUIRE((long long)tokens * topk <= kMoeMaxEntries, "%s: tokens*topk=%lld above %d", fn,
                  (long long)tokens * topk, kMoeMaxEntries);
-    EXL3_REQUIRE(hidden > 0 && inter > 0 && hidden % 128 == 0 && inter % 128 == 0,
-                 "%s: hidden=%d inter=%d must be positive multiples of 128", fn, hidden, inter);
-    EXL3_REQUIRE(KG >= 1 && KG <= 8 && KU >= 1 && KU <= 8 && KD >= 1 && KD <= 8,
-                 "%s: K (gate %d, up %d, down %d) outside 1..8", fn, KG, KU, KD);
-    EXL3_REQUIRE(cb >= 0 && cb <= 2, "%s: codebook=%d outside 0..2", fn, cb);
-    bool tabs_ok = true;
-    for (int j = 0; j < 9; ++j) tabs_ok = tabs_ok && tb.t[j];
-    EXL3_REQUIRE(x && ids && weights && out && tabs_ok, "%s: null pointer", fn);
-    EXL3_REQUIRE(aligned(x, 4) && aligned(out, 4), "%s: misaligned x/out", fn);
     const MoeLayout L = moe_layout(tokens, topk, E, hidden, inter);
     EXL3_REQUIRE_CODE(ws && ws_bytes >= L.total, EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given",
                       fn, L.total, ws ? ws_bytes : (size_t)0);
@@ -543,6 +533,272 @@ int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* w
     return launch_status("exl3 moe combine launch");
 }
 
+// ------------------------------------------------------------ prefill path
+//
+// For batches whose experts get many rows each, the 16-row work units of the
+// decode path decode every expert's weights once per 16 rows with the
+// pair-form GEMV.  The prefill path groups the rows of each expert into tiles
+// of up to 64 / 128 rows and runs the MFMA GEMM kernel (real-valued B
+// fragments, decode once per tile) in its grouped mode:
+//   route    one workgroup: counting sort of the (token, slot) entries by
+//            expert -> compact row -> entry map, row tiles (expert, first row,
+//            rows), the tile count
+//   rotate   xr[p][crow] = fp16(H(x[token] (.) suh_p[e]) / sqrt(128)) for the
+//            gate and up projections, one wave per (row, projection, block)
+//   gate     g32[crow] = fp32 gate output
+//   up       h[crow] = fp16 silu(min(g, L)) * clamp(u, -L, L), rotated with the
+//            down projection's suh
+//   down     y[entry] = fp16 down output
+//   combine  out[t] = sum over the token's valid slots of w * y, fp32, slot order
+// Every grid is a function of the shapes only (tiles past the device count
+// exit at once), so the layer stays capturable in a HIP graph; batches above
+// kMoePrefillChunk entries run as consecutive token chunks.  The reference
+// runs these experts through a host loop over experts (counts.tolist()) into
+// exl3_fat_gemm / exl3_fat_gemm_scatter (src/sglang_exl3/exl3.py:1154-1231,
+// 1234-1344).
+constexpr int kMoePrefillChunk = 16384;  // (token, slot) entries per pipeline pass
+
+__global__ __launch_bounds__(MOE_ROUTE_THREADS) void moe_prefill_route_kernel(const int32_t* ids, int entries,
+                                                                             int E, int mt, int* pos, int* rows,
+                                                                             FatTile* tiles, int* counts) {
+    extern __shared__ __align__(16) int prs[];
+    int* cnt = prs;       // [E]
+    int* off = cnt + E;   // [E] first compact row
+    int* toff = off + E;  // [E] first tile
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += MOE_ROUTE_THREADS) cnt[e] = 0;
+    __syncthreads();
+    const EXL3_GLOBAL int32_t* idg = gptr(ids);
+    EXL3_GLOBAL int* posg = gptr(pos);
+    for (int i = tid; i < entries; i += MOE_ROUTE_THREADS) {
+        const int e = idg[i];
+        posg[i] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
+    }
+    __syncthreads();
+    if (tid < 64) {  // exclusive scans of rows and tiles over the experts, one wave
+        const int chunk = (E + 63) / 64;
+        const int e0 = tid * chunk, e1 = min(E, e0 + chunk);
+        int sr = 0, st = 0;
+        for (int e = e0; e < e1; ++e) {
+            sr += cnt[e];
+            st += (cnt[e] + mt - 1) / mt;
+        }
+        int ir = sr, it = st;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int pr = __shfl_up(ir, d), pt = __shfl_up(it, d);
+            if (tid >= d) {
+                ir += pr;
+                it += pt;
+            }
+        }
+        int r = ir - sr, t = it - st;
+        for (int e = e0; e < e1; ++e) {
+            off[e] = r;
+            toff[e] = t;
+            r += cnt[e];
+            t += (cnt[e] + mt - 1) / mt;
+        }
+        if (tid == 63) {
+            gptr(counts)[0] = it;  // row tiles
+            gptr(counts)[1] = ir;  // routed rows
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < entries; i += MOE_ROUTE_THREADS) {  // the same i as above: own pos[] write
+        const int ps = posg[i];
+        if (ps >= 0) gptr(rows)[off[idg[i]] + ps] = i;
+    }
+    for (int e = tid; e < E; e += MOE_ROUTE_THREADS) {
+        const int c = cnt[e];
+        for (int t = 0; t * mt < c; ++t) {
+            FatTile tl;
+            tl.e = e;
+            tl.crow0 = off[e] + t * mt;
+            tl.nrows = min(mt, c - t * mt);
+            tl.pad = 0;
+            *reinterpret_cast<EXL3_GLOBAL u32x4_t*>(gptr(tiles) + toff[e] + t) = *reinterpret_cast<const u32x4_t*>(&tl);
+        }
+    }
+}
+
+// xr[p][crow][k] = fp16(FWHT(x[token][k] (.) suh_p[e][k]) / sqrt(128)), p = 0 gate, 1 up; one wave per
+// (compact row, projection) walking the row's 128-wide blocks (the loads of the next block are issued
+// before the current block's transform); rows past the routed count exit.
+__global__ __launch_bounds__(256) void moe_prefill_rotate_kernel(const __half* x, const int32_t* ids, const int* rows,
+                                                                const int* counts, const int64_t* suh_g,
+                                                                const int64_t* suh_u, int topk, int hidden,
+                                                                int entries, __half* xr) {
+    const int nblk = hidden >> 7;
+    const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int crow = job >> 1, proj = job & 1;
+    if (crow >= gptr(counts)[1]) return;
+    const int entry = gptr(rows)[crow];
+    const int e = gptr(ids)[entry];
+    const EXL3_GLOBAL __half* suh = gptr(reinterpret_cast<const __half*>(gptr(proj ? suh_u : suh_g)[e])) + 2 * lane;
+    const EXL3_GLOBAL __half* xs = gptr(x) + (size_t)(entry / topk) * hidden + 2 * lane;
+    EXL3_GLOBAL __half* dst = gptr(xr) + ((size_t)proj * entries + crow) * hidden + 2 * lane;
+    __half2 xv = ld_h2(xs), sv = ld_h2(suh);
+    for (int j = 0; j < nblk; ++j) {
+        const __half2 pr = __hmul2(xv, sv);
+        if (j + 1 < nblk) {
+            xv = ld_h2(xs + (j + 1) * 128);
+            sv = ld_h2(suh + (j + 1) * 128);
+        }
+        float a = __low2float(pr), c = __high2float(pr);
+        fwht128_pair_fast(a, c, lane);
+        st_h2(dst + j * 128, h2_rn(a * kHadNorm, c * kHadNorm));
+    }
+}
+
+struct PrefillLayout {
+    int chunk_tokens, entries, mt, max_tiles;
+    size_t counts_off, pos_off, rows_off, tiles_off, xr_off, g_off, h_off, y_off, total;
+};
+
+PrefillLayout prefill_layout(int tokens, int topk, int E, int hidden, int inter) {
+    PrefillLayout L{};
+    L.chunk_tokens = kMoePrefillChunk / topk < 1 ? 1 : kMoePrefillChunk / topk;
+    if (L.chunk_tokens > tokens) L.chunk_tokens = tokens;
+    L.entries = L.chunk_tokens * topk;
+    // 64-row tiles: the 128-row variant holds 67 KB of LDS, so only two
+    // workgroups share a CU, and measured slower per row (config 4, 2048
+    // tokens: 311 us per grouped GEMM launch against 2 x 120 us at 64 rows)
+    L.mt = 64;
+    L.max_tiles = (E < L.entries ? E : L.entries) + L.entries / L.mt;
+    size_t o = kWsScratchOffset;
+    L.counts_off = o;
+    o = align256(o + 4 * sizeof(int));
+    L.pos_off = o;
+    o = align256(o + (size_t)L.entries * sizeof(int));
+    L.rows_off = o;
+    o = align256(o + (size_t)L.entries * sizeof(int));
+    L.tiles_off = o;
+    o = align256(o + (size_t)L.max_tiles * sizeof(FatTile));
+    L.xr_off = o;
+    o = align256(o + (size_t)2 * L.entries * hidden * 2);
+    L.g_off = o;
+    o = align256(o + (size_t)L.entries * inter * 4);
+    L.h_off = o;
+    o = align256(o + (size_t)L.entries * inter * 2);
+    L.y_off = o;
+    o = align256(o + (size_t)L.entries * hidden * 2);
+    L.total = o;
+    return L;
+}
+
+// Rows per active expert (uniform routing estimate) from which a batch takes
+// the prefill path; every batch above the decode path's entry limit does.
+// Graph-timed on config 4 (decode path -> prefill path): B = 64 / 128: 92 /
+// 151 us -> 135 / 158 us; B = 256 / 512 / 1024: 243 / 398 / 772 us -> 217 /
+// 298 / 437 us.
+constexpr double kMoePrefillRowsPerExpert = 16.0;
+
+bool moe_use_prefill(int tokens, int topk, int E) {
+    const int forced = env_int("EXL3_MOE_PREFILL", -1);  // 0: never (decode path), 1: always
+    const long long entries = (long long)tokens * topk;
+    if (entries > kMoeMaxEntries) return true;
+    if (forced >= 0) return forced != 0;
+    const double act = expected_active(tokens, topk, E);
+    return act > 0 && (double)entries / act >= kMoePrefillRowsPerExpert;
+}
+
+int run_moe_prefill(const char* fn, const uint16_t* x, const int32_t* ids, const void* weights, int weights_f16,
+                    const MoeTables& tb, int E, uint16_t* out, int tokens, int topk, int hidden, int inter, int KG,
+                    int KU, int KD, int cb, float limit, void* ws, size_t ws_bytes, hipStream_t st) {
+    const PrefillLayout L = prefill_layout(tokens, topk, E, hidden, inter);
+    EXL3_REQUIRE_CODE(ws && ws_bytes >= L.total, EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given",
+                      fn, L.total, ws ? ws_bytes : (size_t)0);
+    char* w8 = reinterpret_cast<char*>(ws);
+    int* counts = reinterpret_cast<int*>(w8 + L.counts_off);
+    int* pos = reinterpret_cast<int*>(w8 + L.pos_off);
+    int* rows = reinterpret_cast<int*>(w8 + L.rows_off);
+    FatTile* tiles = reinterpret_cast<FatTile*>(w8 + L.tiles_off);
+    __half* xr = reinterpret_cast<__half*>(w8 + L.xr_off);
+    float* g32 = reinterpret_cast<float*>(w8 + L.g_off);
+    __half* h = reinterpret_cast<__half*>(w8 + L.h_off);
+    __half* y = reinterpret_cast<__half*>(w8 + L.y_off);
+    const size_t rsmem = (size_t)3 * E * sizeof(int);
+    int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&moe_prefill_route_kernel), rsmem, "exl3 moe prefill route");
+    if (rc) return rc;
+    const size_t wsz = weights_f16 ? 2 : 4;
+    for (int t0 = 0; t0 < tokens; t0 += L.chunk_tokens) {
+        const int T = tokens - t0 < L.chunk_tokens ? tokens - t0 : L.chunk_tokens;
+        const int entries = T * topk;
+        const int32_t* idc = ids + (size_t)t0 * topk;
+        moe_prefill_route_kernel<<<1, MOE_ROUTE_THREADS, rsmem, st>>>(idc, entries, E, L.mt, pos, rows, tiles,
+                                                                       counts);
+        rc = launch_status("exl3 moe prefill route launch");
+        if (rc) return rc;
+        const long long jobs = (long long)entries * 2;
+        moe_prefill_rotate_kernel<<<(unsigned)((jobs + 3) / 4), 256, 0, st>>>(
+            reinterpret_cast<const __half*>(x) + (size_t)t0 * hidden, idc, rows, counts, tb.t[1], tb.t[4], topk,
+            hidden, entries, xr);
+        rc = launch_status("exl3 moe prefill rotate launch");
+        if (rc) return rc;
+        FatParams p{};
+        p.M = L.max_tiles * L.mt;  // grid.y = max_tiles; rows come from the tiles
+        p.tiles = tiles;
+        p.ntiles = counts;
+        for (int j = 0; j < 9; ++j) p.tabs[j] = tb.t[j];
+        p.g32 = g32;
+        p.rows_map = rows;
+        p.limit = limit;
+        // gate
+        p.gmode = 1;
+        p.a = xr;
+        p.k = hidden;
+        p.n = inter;
+        p.ksteps = hidden / 64;
+        rc = fat_launch(KG, cb, L.mt, p, 1, st);
+        if (rc) return rc;
+        // up, with the SwiGLU and the down projection's input rotation
+        p.gmode = 2;
+        p.a = xr + (size_t)entries * hidden;
+        p.out16 = h;
+        rc = fat_launch(KU, cb, L.mt, p, 1, st);
+        if (rc) return rc;
+        // down, by (token, slot) entry
+        p.gmode = 3;
+        p.a = h;
+        p.k = inter;
+        p.n = hidden;
+        p.ksteps = inter / 64;
+        p.out16 = y;
+        rc = fat_launch(KD, cb, L.mt, p, 1, st);
+        if (rc) return rc;
+        moe_combine_kernel<<<dim3((hidden / 2 + 255) / 256, T), 256, 0, st>>>(
+            y, idc, reinterpret_cast<const char*>(weights) + (size_t)t0 * topk * wsz, weights_f16, topk, E, hidden,
+            reinterpret_cast<__half*>(out) + (size_t)t0 * hidden);
+        rc = launch_status("exl3 moe prefill combine launch");
+        if (rc) return rc;
+    }
+    return EXL3_OK;
+}
+
+int run_moe(const char* fn, const uint16_t* x, const int32_t* ids, const void* weights, int weights_f16,
+            const MoeTables& tb, int E, uint16_t* out, int tokens, int topk, int hidden, int inter, int KG,
+            int KU, int KD, int cb, float limit, void* ws, size_t ws_bytes, hipStream_t st) {
+    EXL3_REQUIRE(tokens >= 1 && topk >= 1, "%s: tokens=%d topk=%d must be >= 1", fn, tokens, topk);
+    EXL3_REQUIRE(E >= 1 && E <= kMoeMaxExperts, "%s: num_experts=%d outside 1..%d", fn, E, kMoeMaxExperts);
+    EXL3_REQUIRE(topk <= kMoePrefillChunk, "%s: topk=%d above %d", fn, topk, kMoePrefillChunk);
+    EXL3_REQUIRE(hidden > 0 && inter > 0 && hidden % 128 == 0 && inter % 128 == 0,
+                 "%s: hidden=%d inter=%d must be positive multiples of 128", fn, hidden, inter);
+    EXL3_REQUIRE(KG >= 1 && KG <= 8 && KU >= 1 && KU <= 8 && KD >= 1 && KD <= 8,
+                 "%s: K (gate %d, up %d, down %d) outside 1..8", fn, KG, KU, KD);
+    EXL3_REQUIRE(cb >= 0 && cb <= 2, "%s: codebook=%d outside 0..2", fn, cb);
+    bool tabs_ok = true;
+    for (int j = 0; j < 9; ++j) tabs_ok = tabs_ok && tb.t[j];
+    EXL3_REQUIRE(x && ids && weights && out && tabs_ok, "%s: null pointer", fn);
+    EXL3_REQUIRE(aligned(x, 4) && aligned(out, 4), "%s: misaligned x/out", fn);
+    if (moe_use_prefill(tokens, topk, E))
+        return run_moe_prefill(fn, x, ids, weights, weights_f16, tb, E, out, tokens, topk, hidden, inter, KG, KU, KD,
+                               cb, limit, ws, ws_bytes, st);
+    return run_moe_decode(fn, x, ids, weights, weights_f16, tb, E, out, tokens, topk, hidden, inter, KG, KU, KD, cb,
+                          limit, ws, ws_bytes, st);
+}
+
 }  // namespace
 }  // namespace exl3
 
@@ -550,6 +806,7 @@ using namespace exl3;
 
 extern "C" size_t exl3_moe_workspace_size(int tokens, int topk, int num_experts, int hidden, int inter) {
     if (tokens < 1 || topk < 1 || num_experts < 1 || hidden < 128 || inter < 128) return 0;
+    if (moe_use_prefill(tokens, topk, num_experts)) return prefill_layout(tokens, topk, num_experts, hidden, inter).total;
     return moe_layout(tokens, topk, num_experts, hidden, inter).total;
 }
 

@@ -478,10 +478,6 @@ def _native_moe_ok(layer, tokens: int, topk: int) -> Optional[str]:
         return f"K per projection {ks} outside integer 1..8"
     if layer._exl3_hidden_size % 128 or layer._exl3_intermediate_local % 128:
         return "hidden/intermediate not multiples of 128"
-    if tokens * topk > 8192:
-        return "more than 8192 routed rows"
-    if not (getattr(layer, "_exl3_use_mcg", False) or getattr(layer, "_exl3_use_mul1", False)):
-        return "3INST experts"
     return None
 
 
@@ -506,7 +502,7 @@ def apply_exl3_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: to
         out = torch.ops.sglang_exl3.exl3_moe_layer(
             x2d, local.to(torch.int32), w.to(torch.float32), *[layer._exl3_ptrs[k] for k in _TABLE_ORDER],
             layer._exl3_k_gate, layer._exl3_k_up, layer._exl3_k_down, bool(layer._exl3_use_mcg),
-            int(layer._exl3_intermediate_local), lim)
+            int(layer._exl3_intermediate_local), lim, int(getattr(layer, "_exl3_codebook", -1)))
         layer._exl3_last_apply = "native"
         return out.to(x.dtype)
     if fused is True:
@@ -619,6 +615,7 @@ class EXL3MoEMethod(FusedMoEMethodBase):
             layer.w13_mul1.zero_()
             layer.w2_mul1.zero_()
         layer._exl3_use_mul1 = use_mul1
+        layer._exl3_codebook = 2 if use_mul1 else 1
         layer._exl3_use_mcg = not use_mul1
         inners = []
         for e in range(int(layer.w13_trellis.shape[0])):

@@ -274,10 +274,11 @@ def p2b_fused_moe_impl(x, out, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, 
 
 def exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs,
                         up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs,
-                        K_gate, K_up, K_down, mcg, intermediate_size, swiglu_limit=0.0):
+                        K_gate, K_up, K_down, mcg, intermediate_size, swiglu_limit=0.0, codebook=-1):
     """Routed-expert MoE layer for a token batch in one call (no host sync).
     topk_ids: [T, topk] local expert ids (outside [0, E) = skipped);
-    topk_weights: [T, topk]; swiglu_limit 0 or inf = no clamp; returns fp16 [T, hidden]."""
+    topk_weights: [T, topk]; swiglu_limit 0 or inf = no clamp; returns fp16 [T, hidden].
+    codebook: 0 = 3INST, 1 = MCG, 2 = mul1; -1 = from `mcg` (MCG or mul1)."""
     name = "exl3_moe_layer"
     tables = (gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs, up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs,
               down_trellis_ptrs, down_suh_ptrs, down_svh_ptrs)
@@ -302,7 +303,8 @@ def exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_p
         rc = lib.exl3_moe_layer(
             xh.data_ptr(), ids.data_ptr(), w.data_ptr(), *[t.data_ptr() for t in tabs], E, out.data_ptr(), T, topk,
             hidden, int(intermediate_size), int(K_gate), int(K_up), int(K_down),
-            _lib.codebook_from_mcg(bool(mcg)), lim, ws.data_ptr(), ws.numel(), _stream_ptr(x))
+            _lib.codebook_from_mcg(bool(mcg)) if int(codebook) < 0 else int(codebook), lim, ws.data_ptr(),
+            ws.numel(), _stream_ptr(x))
     check_ws(rc, name, ws)
     return out
 
@@ -477,10 +479,11 @@ def register_custom_ops() -> bool:
                        up_trellis_ptrs: torch.Tensor, up_suh_ptrs: torch.Tensor, up_svh_ptrs: torch.Tensor,
                        down_trellis_ptrs: torch.Tensor, down_suh_ptrs: torch.Tensor, down_svh_ptrs: torch.Tensor,
                        K_gate: int, K_up: int, K_down: int, mcg: bool, intermediate_size: int,
-                       swiglu_limit: float = 0.0) -> torch.Tensor:
+                       swiglu_limit: float = 0.0, codebook: int = -1) -> torch.Tensor:
         return exl3_moe_layer_impl(x, topk_ids, topk_weights, gate_trellis_ptrs, gate_suh_ptrs, gate_svh_ptrs,
                                    up_trellis_ptrs, up_suh_ptrs, up_svh_ptrs, down_trellis_ptrs, down_suh_ptrs,
-                                   down_svh_ptrs, K_gate, K_up, K_down, mcg, intermediate_size, swiglu_limit)
+                                   down_svh_ptrs, K_gate, K_up, K_down, mcg, intermediate_size, swiglu_limit,
+                                   codebook)
 
     @exl3_moe_layer.register_fake
     def _(x, topk_ids, topk_weights, *rest):

@@ -189,3 +189,17 @@ def test_config5_large_moe_with_shared_expert(K, cb):
     out = ex.layer(x, ids, w)
     torch.cuda.synchronize()
     check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), f"config 5 K={K}")
+
+
+def test_config4_prefill_2048_tokens():
+    """Config 4 at a 2048-token prefill (16384 routed rows, Zipf router): the prefill pipeline;
+    checked on 64 seeded tokens."""
+    print("case: config 4 prefill T=2048", flush=True)
+    B = 2048
+    ids, w = zipf_routing(B, seed=2048)
+    ex = SparseExperts(128, 2048, 768, 3, 1, set(ids.reshape(-1).tolist()), seed=6)
+    x = make_x(B, 2048, seed=60)
+    out = ex.layer(x, ids, w)
+    torch.cuda.synchronize()
+    sel = np.sort(np.random.default_rng(61).choice(B, 64, replace=False))
+    check_close(out.float().cpu().numpy()[sel], ex.ref(x[sel], ids[sel], w[sel]), "config 4 prefill")

@@ -153,3 +153,19 @@ def test_dense_linear_forward_3inst():
     y = lin.forward(torch.from_numpy(x).cuda(), {}, out_dtype=torch.float32)
     torch.cuda.synchronize()
     check_close(y.cpu().numpy(), oracle.matmul(x, oracle.dequant(tr, su, sv, 4, 0, rtz=True)), "3inst linear")
+
+
+def test_moe_method_prefill_batch_stays_native():
+    """A 2048-token top-8 batch (16384 routed rows) runs the device-side prefill
+    pipeline through EXL3MoEMethod.apply, never the host-synced loop."""
+    T, topk, E, hidden, inter, K = 2048, 8, 16, 256, 128, 3
+    method, layer, experts = _build_moe(E, hidden, inter, K, "mul1", seed=99)
+    rng = np.random.default_rng(98)
+    ids = np.stack([rng.choice(E, topk, replace=False) for _ in range(T)]).astype(np.int64)
+    w = rng.random((T, topk)).astype(np.float32)
+    x = make_x(T, hidden, seed=97)
+    out = method.apply(layer, torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    assert layer._exl3_last_apply == "native"
+    sel = np.sort(rng.choice(T, 48, replace=False))
+    check_close(out.float().cpu().numpy()[sel], oracle.moe_ref(x[sel], ids[sel], w[sel], experts), "moe prefill method")

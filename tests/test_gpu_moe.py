@@ -299,3 +299,101 @@ def test_moe_rejects_bad_arguments():
     with pytest.raises(RuntimeError, match="K"):
         torch.ops.sglang_exl3.exl3_moe_layer(torch.zeros((1, 256), dtype=torch.float16, device="cuda"), ids, w,
                                              *ex.tables, 9, 2, 2, True, 128, 0.0)
+
+
+# ------------------------------------------------------------- prefill path
+#
+# Batches whose experts get many rows each (or more than 8192 routed rows) run
+# the prefill pipeline: device-side sort into 64/128-row tiles, one rotation
+# pass, the grouped MFMA GEMM for gate, up (+ SwiGLU + down rotation) and down,
+# then the slot-ordered combine.  EXL3_MOE_PREFILL=1 forces it for small cases.
+
+
+@pytest.mark.parametrize("T,topk,E,hidden,inter,Ks,cb,invalid", [
+    (40, 4, 8, 256, 256, (3, 3, 3), 1, 0),     # ~20 rows per expert: 64-row tiles
+    (300, 2, 4, 256, 128, (2, 3, 4), 2, 3),    # ~150 rows per expert: several 128-row tiles; per-projection K
+    (64, 8, 16, 512, 384, (4, 4, 4), 0, 5),    # 3INST codebook, invalid ids
+    (1, 3, 4, 256, 256, (3, 3, 3), 1, 0),      # a single token through the prefill pipeline
+])
+def test_moe_prefill_path_vs_oracle(T, topk, E, hidden, inter, Ks, cb, invalid, monkeypatch):
+    monkeypatch.setenv("EXL3_MOE_PREFILL", "1")
+    print(f"case: moe prefill T={T} topk={topk} E={E} h={hidden} i={inter} K={Ks} cb={cb}", flush=True)
+    ex = Experts(E, hidden, inter, Ks, cb, seed=T + 3 * E)
+    x = make_x(T, hidden, seed=T + 1)
+    ids, w = _routing(T, topk, E, seed=T * 5 + topk, invalid=invalid)
+    out = _layer_capi(ex, x, ids, w, cb=cb)
+    torch.cuda.synchronize()
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w), f"moe prefill T={T} E={E}")
+
+
+def test_moe_prefill_swiglu_limit(monkeypatch):
+    monkeypatch.setenv("EXL3_MOE_PREFILL", "1")
+    T, topk, E = 48, 2, 4
+    ex = Experts(E, 256, 256, (3, 3, 3), 1, seed=21)
+    x = (make_x(T, 256, seed=22).astype(np.float32) * 2).astype(np.float16)
+    ids, w = _routing(T, topk, E, seed=23)
+    out = _layer_capi(ex, x, ids, w, cb=1, limit=2.0)
+    torch.cuda.synchronize()
+    check_close(out.float().cpu().numpy(), ex.ref(x, ids, w, limit=2.0), "moe prefill limit")
+
+
+def test_moe_prefill_token_chunks_vs_oracle_subset():
+    """16800 routed rows: above one pipeline pass (16384), so two token chunks; checked on 64
+    seeded tokens from both chunks (tokens are independent)."""
+    T, topk, E, hidden, inter = 2100, 8, 32, 256, 128
+    ex = Experts(E, hidden, inter, (3, 3, 3), 1, seed=31)
+    x = make_x(T, hidden, seed=32)
+    ids, w = _routing(T, topk, E, seed=33, invalid=40)
+    out = ex.layer(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    sel = np.sort(np.concatenate([np.random.default_rng(34).choice(2048, 48, replace=False),
+                                  2048 + np.arange(16) * 3]))
+    check_close(out.float().cpu().numpy()[sel], ex.ref(x[sel], ids[sel], w[sel]), "moe prefill chunks")
+
+
+def test_moe_prefill_graph_capturable(monkeypatch):
+    monkeypatch.setenv("EXL3_MOE_PREFILL", "1")
+    T, topk, E = 96, 4, 8
+    ex = Experts(E, 256, 256, (3, 3, 3), 2, seed=41)
+    x = make_x(T, 256, seed=42)
+    ids, w = _routing(T, topk, E, seed=43)
+    xd, idd, wd = (torch.from_numpy(a).cuda() for a in (x, ids, w))
+    a = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gout = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, a), f"prefill graph replay {r} differs from eager"
+        ex.layer(xd, idd, wd)
+        torch.cuda.synchronize()
+    ids2, w2 = _routing(T, topk, E, seed=44)
+    idd.copy_(torch.from_numpy(ids2))
+    wd.copy_(torch.from_numpy(w2))
+    g.replay()
+    torch.cuda.synchronize()
+    check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe prefill graph new routing")
+
+
+def test_moe_prefill_and_decode_paths_agree(monkeypatch):
+    """The same layer through both pipelines (decode: 16-row GEMV units; prefill: MFMA tiles)."""
+    T, topk, E = 64, 4, 8
+    ex = Experts(E, 256, 256, (3, 3, 3), 1, seed=51)
+    x = make_x(T, 256, seed=52)
+    ids, w = _routing(T, topk, E, seed=53)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("EXL3_MOE_PREFILL", mode)
+        outs[mode] = _layer_capi(ex, x, ids, w, cb=1).float().cpu().numpy()
+    ref = ex.ref(x, ids, w)
+    check_close(outs["0"], ref, "decode path")
+    check_close(outs["1"], ref, "prefill path")
