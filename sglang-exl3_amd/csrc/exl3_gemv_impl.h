@@ -213,13 +213,12 @@ __device__ __forceinline__ void load_words(const EXL3_GLOBAL uint32_t* p, uint32
     }
 }
 
-// Request the weight words of a wave's first D steps.  Loads are unconditional,
-// clamped to the last step, so the number in flight is static and each use
-// waits only for its own group.
-template <int K, int NS>
-__device__ __forceinline__ void prime_weights(uint32_t (&w)[gv_depth<K>()][K], const EXL3_GLOBAL uint32_t* tb,
+// Request the weight words of a wave's first D steps (D: the depth of the
+// register ring w).  Loads are unconditional, clamped to the last step, so the
+// number in flight is static and each use waits only for its own group.
+template <int K, int NS, int D>
+__device__ __forceinline__ void prime_weights(uint32_t (&w)[D][K], const EXL3_GLOBAL uint32_t* tb,
                                               size_t step_stride) {
-    constexpr int D = gv_depth<K>();
     constexpr int last = NS - 1;
 #pragma unroll
     for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < last ? d : last) * step_stride, w[d]);
@@ -251,13 +250,13 @@ __device__ __forceinline__ void mv_frags(const uint32_t* buf, const uint32_t* mi
 // fragments and multiply with the staged activations.  Software-pipelined and
 // fully unrolled: each step decodes its words, then reuses their registers to
 // request the words of step s + D, so D - 1 groups stay in flight while it
-// decodes.  a_base[rb]: this lane's A fragments of row block rb in the LDS
-// staging buffer; rows with a_live false read nothing and multiply zeros.
-template <int K, int CB, int MB, int NS>
-__device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[gv_depth<K>()][K], const EXL3_GLOBAL uint32_t* tb,
+// decodes (D: the depth of the register ring w).  a_base[rb]: this lane's A
+// fragments of row block rb in the LDS staging buffer; rows with a_live false
+// read nothing and multiply zeros.
+template <int K, int CB, int MB, int NS, int D>
+__device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[D][K], const EXL3_GLOBAL uint32_t* tb,
                                                   size_t step_stride, const _Float16* const (&a_base)[MB],
                                                   const bool (&a_live)[MB], float4_t (&acc)[MB][2]) {
-    constexpr int D = gv_depth<K>();
     const int lane = threadIdx.x & 63;
     // lane holding the previous group of the same tile (q - 1 mod 8), as a
     // ds_bpermute byte address

@@ -19,6 +19,30 @@ int moe_launch_K6(int, int, const MoeParams&, hipStream_t);
 int moe_launch_K7(int, int, const MoeParams&, hipStream_t);
 int moe_launch_K8(int, int, const MoeParams&, hipStream_t);
 
+int moe_fused_launch_K1(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K2(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K3(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K4(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K5(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K6(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K7(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+int moe_fused_launch_K8(int, int, int, const MoeParams&, const MoeParams&, hipStream_t);
+
+int moe_fused_launch(int K, int cb, int nsg, int nsd, const MoeParams& pg, const MoeParams& pd, hipStream_t st) {
+    switch (K) {
+        case 1: return moe_fused_launch_K1(cb, nsg, nsd, pg, pd, st);
+        case 2: return moe_fused_launch_K2(cb, nsg, nsd, pg, pd, st);
+        case 3: return moe_fused_launch_K3(cb, nsg, nsd, pg, pd, st);
+        case 4: return moe_fused_launch_K4(cb, nsg, nsd, pg, pd, st);
+        case 5: return moe_fused_launch_K5(cb, nsg, nsd, pg, pd, st);
+        case 6: return moe_fused_launch_K6(cb, nsg, nsd, pg, pd, st);
+        case 7: return moe_fused_launch_K7(cb, nsg, nsd, pg, pd, st);
+        case 8: return moe_fused_launch_K8(cb, nsg, nsd, pg, pd, st);
+    }
+    set_error("exl3 moe: K=%d outside 1..8", K);
+    return EXL3_ERR_UNSUPPORTED;
+}
+
 int moe_launch(int K, int cb, int ns, const MoeParams& p, hipStream_t st) {
     switch (K) {
         case 1: return moe_launch_K1(cb, ns, p, st);
@@ -280,6 +304,36 @@ int moe_grid_size(const void* fn, int threads, size_t smem) {
     return (forced > 0 ? forced : per_cu) * cus;
 }
 
+int moe_fused_grid_size(const void* fn, size_t smem) {
+    const int est = moe_grid_size(fn, 256, smem);
+    if (est <= 0) return est;
+    struct Entry {
+        const void* fn;
+        size_t smem;
+        int dev, resident;
+    };
+    static Entry cache[32];
+    static int ncache = 0;
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error("exl3 moe: hipGetDevice failed");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    for (int j = 0; j < ncache; ++j)
+        if (cache[j].fn == fn && cache[j].smem == smem && cache[j].dev == dev)
+            return est < cache[j].resident ? est : cache[j].resident;
+    int cus = 0, nb = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 256, smem) != hipSuccess || nb < 1 || cus < 1) {
+        set_error("exl3 moe: occupancy query failed");
+        return -1;
+    }
+    if (ncache < 32) cache[ncache++] = Entry{fn, smem, dev, nb * cus};
+    return est < nb * cus ? est : nb * cus;
+}
+
 namespace {
 
 constexpr int kMoeMaxExperts = 4096;
@@ -363,7 +417,7 @@ struct MoeLayout {
     int entries, max_units;
     bool rot, fc;
     MoePlan gu, dn;
-    size_t route_off, units_off, rows_off, tokv_off, h_off, y_off, xr_off, part_off, total;
+    size_t route_off, units_off, rows_off, tokv_off, h_off, y_off, xr_off, part_off, part_dn_off, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -404,10 +458,15 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     L.rot = tokens >= env_int("EXL3_MOE_ROT_TOKENS", kMoeRotTokens);
     L.xr_off = o;
     if (L.rot) o = align256(o + (size_t)2 * L.entries * hidden * 2);
+    // split partials: one region that the gate/up and down launches reuse in
+    // turn; one token gets a second one for the down items, which run
+    // alongside the gate/up items in the fused one-token launch
     L.part_off = o;
     const size_t pg = (size_t)(inter / 128) * 2 * L.gu.splits;
     const size_t pd = (size_t)(hidden / 128) * 1 * L.dn.splits;
-    o = align256(o + (pg > pd ? pg : pd) * L.entries * 128 * sizeof(float));
+    o = align256(o + (tokens == 1 ? pg : (pg > pd ? pg : pd)) * L.entries * 128 * sizeof(float));
+    L.part_dn_off = tokens == 1 ? o : L.part_off;
+    if (tokens == 1) o = align256(o + pd * L.entries * 128 * sizeof(float));
     L.total = o;
     return L;
 }
@@ -477,6 +536,22 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.E = E;
     p.tabs = tb;
 
+    // One token, one K for all three projections: gate/up and down can run
+    // in one persistent launch (moe_fused_direct_kernel), opt-in with env
+    // EXL3_MOE_FUSED=1.  It gives the same bits but is not the default:
+    // graph-timed on config 4 (layers back to back) the fused kernel takes
+    // 22.4 us against 11.6 + 9.8 us for the two launches, whose boundary
+    // costs ~0.3 us; the down items, started early, decode more slowly next
+    // to the running gate/up items than the down launch does alone.
+    // readiness flag rows 1 KB apart: the polls of one unit's down items
+    // stay off the lines of other units' flags and of the hand-off counters
+    int ready_stride = env_int("EXL3_MOE_READY_STRIDE", 256);
+    if (ready_stride < inter / 128) ready_stride = inter / 128;
+    const bool fused = direct && KG == KU && KU == KD && moe_fused_steps_ok(L.gu.ns) && moe_fused_steps_ok(L.dn.ns) &&
+                       L.gu.kw == 1 && L.dn.kw == 1 &&
+                       (size_t)topk * (inter / 128 + hidden / 128 + ready_stride + 1) + 256 <= kWsMaxCounters &&
+                       env_int("EXL3_MOE_FUSED", 0) != 0;
+
     // 3. gate + up (+ SwiGLU + down input rotation)
     p.mode = MOE_GATE_UP;
     p.x = L.rot ? xr : reinterpret_cast<const __half*>(x);
@@ -489,7 +564,20 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.kw = L.gu.kw;
     p.bx_per_item = L.gu.bpi;
     int rc;
-    if (KG == KU) {
+    MoeParams pg = p;  // the gate/up pass, kept for the fused launch
+    pg.proj_base = 0;
+    pg.proj_launch = 2;
+    if (fused) {
+        // counters: [gate/up hand-off | down hand-off | readiness flags | done counts]
+        const int nbg = inter / 128, nbd = hidden / 128;
+        int* c0 = reinterpret_cast<int*>(w8);
+        pg.ready = c0 + (((size_t)topk * (nbg + nbd) + 255) & ~(size_t)255);
+        pg.done = pg.ready + (size_t)topk * ready_stride;
+        pg.ready_nblk = nbg;
+        pg.ready_stride = ready_stride;
+        pg.poll_sleep = env_int("EXL3_MOE_POLL_SLEEP", 1);
+        pg.prime_late = env_int("EXL3_MOE_PRIME_LATE", 0);
+    } else if (KG == KU) {
         p.proj_base = 0;
         p.proj_launch = 2;
         rc = moe_launch(KG, cb, L.gu.ns, p, st);
@@ -523,7 +611,20 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.weights = weights;
     p.weights_f16 = weights_f16;
     p.final_out = reinterpret_cast<__half*>(out);
-    rc = moe_launch(KD, cb, L.dn.ns, p, st);
+    if (fused) {
+        p.counters = reinterpret_cast<int*>(w8) + (size_t)topk * (inter / 128);
+        p.partials = reinterpret_cast<float*>(w8 + L.part_dn_off);
+        p.ready = pg.ready;
+        p.done = pg.done;
+        p.ready_nblk = pg.ready_nblk;
+        p.ready_stride = pg.ready_stride;
+        p.poll_sleep = pg.poll_sleep;
+        p.prime_late = pg.prime_late;
+        p.dn_items_per_unit = ((hidden / 128) / L.dn.bpi) * L.dn.splits;
+        rc = moe_fused_launch(KD, cb, L.gu.ns, L.dn.ns, pg, p, st);
+    } else {
+        rc = moe_launch(KD, cb, L.dn.ns, p, st);
+    }
     if (rc) return rc;
     if (L.fc) return EXL3_OK;
 

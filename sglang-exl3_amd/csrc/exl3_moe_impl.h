@@ -110,6 +110,16 @@ struct MoeParams {
     const int32_t* ids;
     int E;
     MoeTables tabs;
+    // Gate/up and down in one launch (moe_fused_direct_kernel): readiness
+    // flags of the h blocks [units][ready_nblk] and per-unit counts of down
+    // items past their wait, both in the workspace's zeroed counter region.
+    int* ready;
+    int* done;
+    int ready_nblk;
+    int ready_stride;  // ints between the flag rows of two units
+    int poll_sleep;    // s_sleep(8) calls between two polls
+    int prime_late;    // down items request their weights after the wait
+    int dn_items_per_unit;
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
@@ -131,28 +141,80 @@ __device__ __forceinline__ __half2 ld_h2_ptr(const void* base, int idx) {
     return ld_h2(gptr(reinterpret_cast<const __half*>(base)) + idx);
 }
 
-// Persistent over work items (unit, column block, projection, k-split): the
-// grid is sized to the device, the item count comes from the routing kernel,
-// so no workgroup is launched for an inactive expert.  Per item: stage the
-// unit's activation rows (rotated by the projection's suh unless the input
-// arrives rotated), decode + MFMA the split's k range for 128 columns, store
-// fp32 partial rows; the last of nproj * S arrivals of (unit, column block)
-// runs the epilogue.
-template <int K, int CB, int NS, int MODE, int KW>
-__global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
-    constexpr int ROWS = MOE_UNIT_ROWS;
-    extern __shared__ __align__(16) unsigned char mv_smem[];
-    __shared__ int is_last;
+// fp16 pair through a device-coherent 32-bit load / store (data handed from
+// one workgroup to another inside a launch).
+__device__ __forceinline__ __half2 ld_h2_coherent(const EXL3_GLOBAL __half* ptr) {
+    const uint32_t u = __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<__half*>((const __half*)ptr)),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *reinterpret_cast<const __half2*>(&u);
+}
+__device__ __forceinline__ void st_h2_coherent(EXL3_GLOBAL __half* ptr, __half2 v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>((__half*)ptr), *reinterpret_cast<const uint32_t*>(&v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
+// Polls (each followed by an s_sleep of ~0.2 us) after which a fused down item
+// stops waiting for its h blocks (about 0.25 s: far beyond any gate/up pass;
+// a bound so that every wave exits even if a producer never ran).
+constexpr int kMoeWaitPolls = 1 << 20;
+
+// Wait until the readiness flags f[j0..j1] are all set (one thread).
+__device__ __forceinline__ void wait_ready(const int* f, int j0, int j1, int nsleep) {
+    for (int it = 0; it < kMoeWaitPolls; ++it) {
+        bool ok = true;
+        for (int j = j0; j <= j1; ++j)
+            ok = ok && __hip_atomic_load(const_cast<int*>(f) + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+        if (ok) return;
+        for (int z = 0; z < nsleep; ++z) __builtin_amdgcn_s_sleep(8);
+    }
+}
+
+// Weight steps a MoE work item keeps in flight: every step of the item up to
+// `words` words per lane (24 for a directly routed token, 12 for the routed
+// down pass, two steps for the routed gate/up passes, whose multi-row code
+// spills beyond that).  A small pass has about one item per workgroup and its
+// weight stream is latency-bound, so the bytes in flight set its rate.
+template <int K, int NS, int MODE>
+__host__ __device__ constexpr int moe_depth() {
+    constexpr int words = (MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT) ? 24 : MODE == MV_DOWN ? 12 : 2 * K;
+    constexpr int budget = words / K > 2 ? words / K : 2;
+    return NS < budget ? NS : budget;
+}
+
+// Valid slots of a directly routed token (ids in [0, E)).
+__device__ __forceinline__ int direct_valid_slots(const MoeParams& p) {
+    int v = 0;
+    for (int sl = 0; sl < p.topk; ++sl) {
+        const int e = uniform_i(gptr(p.ids)[sl]);
+        v += e >= 0 && e < p.E;
+    }
+    return v;
+}
+
+// fp16 zero row of n columns (workgroup-wide).
+__device__ __forceinline__ void zero_row(__half* out, int n) {
+    for (int c = threadIdx.x; c < n / 2; c += blockDim.x) reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(out))[c] = 0u;
+}
+
+// One work item (unit, column block group, projection, k-split) of a
+// projection pass: stage the unit's activation rows (rotated by the
+// projection's suh unless the input arrives rotated), decode + MFMA the
+// split's k range for each of the group's 128-column blocks, store fp32
+// partial rows; the last of nproj * S arrivals of (unit, column block) runs
+// the epilogue.  `first`: this is the workgroup's first item (no barrier for
+// the LDS of a previous one).  FUSED: the gate/up and down passes share one
+// launch (moe_fused_direct_kernel): gate/up epilogues publish each finished
+// 128-wide block of h, and down items wait for the blocks they read.
+template <int K, int CB, int NS, int MODE, int KW, bool FUSED>
+__device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned char* mv_smem, int direct_valid,
+                                         bool first) {
+    constexpr int ROWS = MOE_UNIT_ROWS;
+    __shared__ int is_last;
     constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
-    const int nunits = direct ? p.topk : uniform_i(gptr(p.rt.counts)[1]);
     const int nblk_n = p.n >> 7;
     const int BPI = p.bx_per_item, ngroups = nblk_n / BPI;
     const int S = p.splits, P = p.proj_launch;
     const int per_unit = ngroups * P * S;
-    const int total = nunits * per_unit;
-    if ((int)blockIdx.x >= total) return;
-
     const int k = p.k, n = p.n;
     constexpr int kw = KW;  // k waves (p.kw)
     constexpr int nsteps = NS;
@@ -166,7 +228,6 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     constexpr bool pre_rotated = MODE != MV_GU && MODE != MV_GU_DIRECT;  // input rows arrive rotated
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const size_t split_stride = (size_t)p.entries * 128;
-
     const int nblk128 = kts_wg >> 3;
     _Float16* xs = reinterpret_cast<_Float16*>(mv_smem);
     const int xs_halves = kts_wg * 4 * ROWS * 8;
@@ -174,311 +235,390 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     float* ybuf = xsum + ((ROWS * nblk128 + 3) & ~3);
     if (tid < 8) xs[xs_halves + tid] = (_Float16)0.0f;
     const EXL3_GLOBAL int* rows_g = gptr(p.rt.rows);
-    // one token routed directly: its valid slots (the fused combine's count);
-    // with none, workgroup 0 writes the zero output row
-    int direct_valid = 0;
-    if (down && direct) {
-        for (int sl = 0; sl < p.topk; ++sl) {
-            const int e = uniform_i(gptr(p.ids)[sl]);
-            direct_valid += e >= 0 && e < p.E;
-        }
-        if (direct_valid == 0) {
-            if (blockIdx.x == 0 && p.fc)
-                for (int c = tid; c < n / 2; c += blockDim.x)
-                    reinterpret_cast<EXL3_GLOBAL uint32_t*>(gptr(p.final_out))[c] = 0u;
-            return;
-        }
+
+    const int u = it / per_unit;
+    int rem = it - u * per_unit;
+    const int bg = rem / (P * S);
+    rem -= bg * P * S;
+    const int pl = rem / S, sidx = rem - pl * S;
+    const int proj = p.proj_base + pl;
+
+    const int pb = down ? 6 : 3 * proj;
+    int m, crow0;
+    const void *tp, *suh, *ev0p, *ev1p, *ev2p;
+    if (direct) {
+        const int e = uniform_i(gptr(p.ids)[u]);
+        if (e < 0 || e >= p.E) return;  // skipped slot (uniform over the workgroup)
+        m = 1;
+        crow0 = u;
+        auto tab = [&](int j) { return uniform_p(reinterpret_cast<const void*>(gptr(p.tabs.t[j])[e])); };
+        tp = tab(pb);
+        suh = tab(pb + 1);
+        ev0p = tab(down ? 8 : 2);
+        ev1p = tab(5);
+        ev2p = tab(7);
+    } else {
+        const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
+        m = uniform_i(ud->nrows);
+        crow0 = uniform_i(ud->crow0);
+        tp = uniform_p(ud->ptr[pb]);
+        suh = uniform_p(ud->ptr[pb + 1]);
+        ev0p = uniform_p(ud->ptr[down ? 8 : 2]);  // svh of down / gate
+        ev1p = uniform_p(ud->ptr[5]);             // svh of up
+        ev2p = uniform_p(ud->ptr[7]);             // suh of down (its input rotation)
     }
+    const uint32_t* trellis = reinterpret_cast<const uint32_t*>(tp);
+    const int kt_wg0 = sidx * kts_wg;
+    const int kt_w0 = kt_wg0 + kwi * 4 * nsteps;
+    const int bx0 = bg * BPI;
+    auto tiles = [&](int bx) {
+        return gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + bx * 8 + cw * 2 + (i >> 3)) * (8 * K) + K * q;
+    };
+    if (!first) __syncthreads();  // the previous item is done with LDS
 
-    // Items in rounds over the grid, snake order (round r: workgroup b takes
-    // item r G + b for even r, r G + G - 1 - b for odd r), so the workgroup with
-    // the last (lightest) item of a round takes the first (heaviest) of the next.
-    const int G = gridDim.x, b0 = blockIdx.x;
-    for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0)) {
-        const int u = it / per_unit;
-        int rem = it - u * per_unit;
-        const int bg = rem / (P * S);
-        rem -= bg * P * S;
-        const int pl = rem / S, sidx = rem - pl * S;
-        const int proj = p.proj_base + pl;
+    // the entries of the unit's rows, one per lane, looked up once (the
+    // row loops below read them with readlane instead of a dependent load
+    // per row)
+    const bool by_entry = !down && !direct && (pre_rotated || !p.single_token);
+    const int ent_lane = (by_entry && lane < m) ? rows_g[crow0 + lane] : 0;
+    auto x_row = [&](int row) -> const EXL3_GLOBAL __half* {
+        if (down) return gptr(p.x) + (size_t)(crow0 + row) * k;
+        if (!by_entry) return gptr(p.x);
+        const int entry = __builtin_amdgcn_readlane(ent_lane, row);
+        if (pre_rotated) return gptr(p.x) + ((size_t)proj * p.entries + entry) * k;
+        return gptr(p.x) + (size_t)(entry / p.topk) * k;
+    };
 
-        const int pb = down ? 6 : 3 * proj;
-        int m, crow0;
-        const void *tp, *suh, *ev0p, *ev1p, *ev2p;
-        if (direct) {
-            const int e = uniform_i(gptr(p.ids)[u]);
-            if (e < 0 || e >= p.E) continue;  // skipped slot (uniform over the workgroup)
-            m = 1;
-            crow0 = u;
-            auto tab = [&](int j) { return uniform_p(reinterpret_cast<const void*>(gptr(p.tabs.t[j])[e])); };
-            tp = tab(pb);
-            suh = tab(pb + 1);
-            ev0p = tab(down ? 8 : 2);
-            ev1p = tab(5);
-            ev2p = tab(7);
-        } else {
-            const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
-            m = uniform_i(ud->nrows);
-            crow0 = uniform_i(ud->crow0);
-            tp = uniform_p(ud->ptr[pb]);
-            suh = uniform_p(ud->ptr[pb + 1]);
-            ev0p = uniform_p(ud->ptr[down ? 8 : 2]);  // svh of down / gate
-            ev1p = uniform_p(ud->ptr[5]);             // svh of up
-            ev2p = uniform_p(ud->ptr[7]);             // suh of down (its input rotation)
-        }
-        const uint32_t* trellis = reinterpret_cast<const uint32_t*>(tp);
-        const int kt_wg0 = sidx * kts_wg;
-        const int kt_w0 = kt_wg0 + kwi * 4 * nsteps;
-        const int bx0 = bg * BPI;
-        auto tiles = [&](int bx) {
-            return gptr(trellis) + ((size_t)(kt_w0 + g) * ntiles + bx * 8 + cw * 2 + (i >> 3)) * (8 * K) + K * q;
-        };
-        if (it != (int)blockIdx.x) __syncthreads();  // the previous item is done with LDS
-
-        // the entries of the unit's rows, one per lane, looked up once (the
-        // row loops below read them with readlane instead of a dependent load
-        // per row)
-        const bool by_entry = !down && !direct && (pre_rotated || !p.single_token);
-        const int ent_lane = (by_entry && lane < m) ? rows_g[crow0 + lane] : 0;
-        auto x_row = [&](int row) -> const EXL3_GLOBAL __half* {
-            if (down) return gptr(p.x) + (size_t)(crow0 + row) * k;
-            if (!by_entry) return gptr(p.x);
-            const int entry = __builtin_amdgcn_readlane(ent_lane, row);
-            if (pre_rotated) return gptr(p.x) + ((size_t)proj * p.entries + entry) * k;
-            return gptr(p.x) + (size_t)(entry / p.topk) * k;
-        };
-
-        // 1. activation loads (up to MV_PRE blocks per wave, all in flight),
-        //    then the first column block's weights
-        const int nrot = m * nblk128;
-        __half2 xpre[MV_PRE], spre[MV_PRE];
+    // 1. activation loads (up to MV_PRE blocks per wave, all in flight),
+    //    then the first column block's weights.  A down item of the fused
+    //    launch requests its weights first, then waits until the gate/up
+    //    epilogues have published the h blocks of its k range (their
+    //    stores were device-coherent, so it reads them coherently too).
+    constexpr bool wait_h = FUSED && down;
+    auto ld_x = [&](const EXL3_GLOBAL __half* ptr) -> __half2 {
+        if constexpr (wait_h) return ld_h2_coherent(ptr);
+        else return ld_h2(ptr);
+    };
+    const int nrot = m * nblk128;
+    __half2 xpre[MV_PRE], spre[MV_PRE];
+    auto preload = [&]() {
 #pragma unroll
         for (int j = 0; j < MV_PRE; ++j) {
             const int b = wave + j * nwaves;
             if (b < nrot) {
                 const int row = b / nblk128, bb = b - row * nblk128;
                 const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
-                xpre[j] = ld_h2(x_row(row) + kg);
+                xpre[j] = ld_x(x_row(row) + kg);
                 if (!pre_rotated) spre[j] = ld_h2_ptr(suh, kg);
             }
         }
-        uint32_t w[gv_depth<K>()][K];
-        prime_weights<K, NS>(w, tiles(bx0), step_stride);
-
-        // 2. stage the rows in A-fragment order once for all column blocks of
-        //    the item (rotated here unless they arrive rotated)
-        auto stage = [&](int b, __half2 xv, __half2 sv) {
-            const int row = b / nblk128, bb = b - row * nblk128;
-            const int kk = bb * 128 + 2 * lane;
-            _Float16 ha, hc;
-            if (pre_rotated) {
-                ha = (_Float16)__low2float(xv);
-                hc = (_Float16)__high2float(xv);
-            } else {
-                const __half2 pr = __hmul2(xv, sv);
-                float fa = __low2float(pr), fc = __high2float(pr);
-                fwht128_pair_fast(fa, fc, lane);
-                ha = f16_rn(fa * kHadNorm);
-                hc = f16_rn(fc * kHadNorm);
-            }
-            const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
-            xs[ia] = ha;
-            xs[ia + 1] = ha;
-            xs[ic] = hc;
-            xs[ic + 1] = hc;
-            if constexpr (CB == 2) {
-                const float t = wave_sum((float)ha + (float)hc);
-                if (lane == 0) xsum[b] = t;
-            }
-        };
-#pragma unroll
-        for (int j = 0; j < MV_PRE; ++j) {
-            const int b = wave + j * nwaves;
-            if (b < nrot) stage(b, xpre[j], spre[j]);
-        }
-        for (int b = wave + MV_PRE * nwaves; b < nrot; b += nwaves) {
-            const int row = b / nblk128, bb = b - row * nblk128;
-            const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
-            const __half2 sv = pre_rotated ? __half2{} : ld_h2_ptr(suh, kg);
-            stage(b, ld_h2(x_row(row) + kg), sv);
-        }
+    };
+    uint32_t w[moe_depth<K, NS, MODE>()][K];
+    if constexpr (wait_h) {
+        if (!p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
+        if (tid == 0)
+            wait_ready(p.ready + (size_t)u * p.ready_stride, kt_wg0 >> 3, (kt_wg0 + kts_wg - 1) >> 3, p.poll_sleep);
         __syncthreads();
+        if (p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
+        preload();
+    } else {
+        preload();
+        prime_weights<K, NS>(w, tiles(bx0), step_stride);
+    }
 
-        const bool live = i < m;
-        const _Float16* a_base[1] = {xs + (size_t)((live ? i : 0) * kts_wg + kwi * 4 * nsteps + g) * 4 * 8};
-        const bool a_live[1] = {live};
-        for (int bx = bx0; bx < bx0 + BPI; ++bx) {
-            if (bx != bx0) {
-                __syncthreads();  // the previous block is done with ybuf
-                prime_weights<K, NS>(w, tiles(bx), step_stride);
+    // 2. stage the rows in A-fragment order once for all column blocks of
+    //    the item (rotated here unless they arrive rotated)
+    auto stage = [&](int b, __half2 xv, __half2 sv) {
+        const int row = b / nblk128, bb = b - row * nblk128;
+        const int kk = bb * 128 + 2 * lane;
+        _Float16 ha, hc;
+        if (pre_rotated) {
+            ha = (_Float16)__low2float(xv);
+            hc = (_Float16)__high2float(xv);
+        } else {
+            const __half2 pr = __hmul2(xv, sv);
+            float fa = __low2float(pr), fc = __high2float(pr);
+            fwht128_pair_fast(fa, fc, lane);
+            ha = f16_rn(fa * kHadNorm);
+            hc = f16_rn(fc * kHadNorm);
+        }
+        const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
+        xs[ia] = ha;
+        xs[ia + 1] = ha;
+        xs[ic] = hc;
+        xs[ic + 1] = hc;
+        if constexpr (CB == 2) {
+            const float t = wave_sum((float)ha + (float)hc);
+            if (lane == 0) xsum[b] = t;
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < MV_PRE; ++j) {
+        const int b = wave + j * nwaves;
+        if (b < nrot) stage(b, xpre[j], spre[j]);
+    }
+    for (int b = wave + MV_PRE * nwaves; b < nrot; b += nwaves) {
+        const int row = b / nblk128, bb = b - row * nblk128;
+        const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
+        const __half2 sv = pre_rotated ? __half2{} : ld_h2_ptr(suh, kg);
+        stage(b, ld_x(x_row(row) + kg), sv);
+    }
+    __syncthreads();
+
+    const bool live = i < m;
+    const _Float16* a_base[1] = {xs + (size_t)((live ? i : 0) * kts_wg + kwi * 4 * nsteps + g) * 4 * 8};
+    const bool a_live[1] = {live};
+    for (int bx = bx0; bx < bx0 + BPI; ++bx) {
+        if (bx != bx0) {
+            __syncthreads();  // the previous block is done with ybuf
+            prime_weights<K, NS>(w, tiles(bx), step_stride);
+        }
+        // epilogue vectors of this block, requested now so they are in
+        // registers at the end
+        const int c0 = bx * 128 + 2 * lane;
+        const __half2 ev0 = ld_h2_ptr(ev0p, c0);
+        __half2 ev1 = __half2{}, ev2 = __half2{};
+        if (!down) {
+            ev1 = ld_h2_ptr(ev1p, c0);
+            ev2 = ld_h2_ptr(ev2p, c0);
+        }
+
+        // 3. decode + MFMA (rows >= m read nothing and multiply zeros)
+        float4_t acc[1][2];
+        acc[0][0] = float4_t{0.f, 0.f, 0.f, 0.f};
+        acc[0][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+        decode_mfma_steps<K, CB, 1, NS>(w, tiles(bx), step_stride, a_base, a_live, acc);
+
+        // 4. k waves summed through LDS, mul1 affine map, partial rows out
+        //    (one k wave: straight from the accumulators, no LDS tile, so
+        //    four workgroups fit a CU)
+        float* part =
+            p.partials + ((size_t)(bx * p.nproj + proj) * S + sidx) * split_stride + (size_t)crow0 * 128;
+        if constexpr (KW == 1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 4 * g + r;
+                if (row >= m) continue;
+                float sx = 0.f;
+                if constexpr (CB == 2)
+                    for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                    float v = acc[0][c][r];
+                    if constexpr (CB == 2) v = v * kMul1Kinv + kMul1Delta * sx;
+                    coherent_store(part + row * 128 + col, v);
+                }
             }
-            // epilogue vectors of this block, requested now so they are in
-            // registers at the end
-            const int c0 = bx * 128 + 2 * lane;
-            const __half2 ev0 = ld_h2_ptr(ev0p, c0);
-            __half2 ev1 = __half2{}, ev2 = __half2{};
-            if (!down) {
-                ev1 = ld_h2_ptr(ev1p, c0);
-                ev2 = ld_h2_ptr(ev2p, c0);
-            }
-
-            // 3. decode + MFMA (rows >= m read nothing and multiply zeros)
-            float4_t acc[1][2];
-            acc[0][0] = float4_t{0.f, 0.f, 0.f, 0.f};
-            acc[0][1] = float4_t{0.f, 0.f, 0.f, 0.f};
-            decode_mfma_steps<K, CB, 1, NS>(w, tiles(bx), step_stride, a_base, a_live, acc);
-
-            // 4. k waves summed through LDS, mul1 affine map, partial rows out
-            //    (one k wave: straight from the accumulators, no LDS tile, so
-            //    four workgroups fit a CU)
-            float* part =
-                p.partials + ((size_t)(bx * p.nproj + proj) * S + sidx) * split_stride + (size_t)crow0 * 128;
-            if constexpr (KW == 1) {
+        }
+        else {
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 4 * g + r;
-                    if (row >= m) continue;
+                    const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
+                    if (row < m) ybuf[(kwi * ROWS + row) * 128 + col] = acc[0][c][r];
+                }
+            __syncthreads();
+            for (int idx = tid; idx < m * 128; idx += nthreads) {
+                float v = ybuf[idx];
+                for (int j = 1; j < kw; ++j) v += ybuf[j * ROWS * 128 + idx];
+                if constexpr (CB == 2) {
+                    const int row = idx >> 7;
                     float sx = 0.f;
-                    if constexpr (CB == 2)
-                        for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                        float v = acc[0][c][r];
-                        if constexpr (CB == 2) v = v * kMul1Kinv + kMul1Delta * sx;
-                        coherent_store(part + row * 128 + col, v);
-                    }
+                    for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+                    v = v * kMul1Kinv + kMul1Delta * sx;
                 }
-            }
-            else {
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int row = 4 * g + r;
-                        const int col = cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                        if (row < m) ybuf[(kwi * ROWS + row) * 128 + col] = acc[0][c][r];
-                    }
-                __syncthreads();
-                for (int idx = tid; idx < m * 128; idx += nthreads) {
-                    float v = ybuf[idx];
-                    for (int j = 1; j < kw; ++j) v += ybuf[j * ROWS * 128 + idx];
-                    if constexpr (CB == 2) {
-                        const int row = idx >> 7;
-                        float sx = 0.f;
-                        for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
-                        v = v * kMul1Kinv + kMul1Delta * sx;
-                    }
-                    coherent_store(part + idx, v);
-                }
-            }
-
-            // 5. hand-off: the last of nproj * S arrivals for (unit, column
-            //    block) finishes
-            wait_stores();
-            __syncthreads();
-            int* ctr = p.counters + (size_t)u * nblk_n + bx;
-            if (tid == 0) {
-                const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                is_last = (old == p.nproj * S - 1);
-            }
-            __syncthreads();
-            if (!is_last) continue;
-            if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-            // 6. epilogue, one row per wave, 2 columns per lane; split partials
-            //    of a row are all requested before the first add (one round
-            //    trip) and summed in split order
-            auto sum_rows = [&](int np, int crow, float2* out) {
-                constexpr int G = 8;
-                for (int s0 = 0; s0 < S; s0 += G) {
-                    float2 v[2][G];
-#pragma unroll
-                    for (int pj = 0; pj < 2; ++pj)
-#pragma unroll
-                        for (int j = 0; j < G; ++j)
-                            if (pj < np && s0 + j < S)
-                                v[pj][j] = coherent_load2(
-                                    p.partials + ((size_t)(bx * p.nproj + pj) * S + s0 + j) * split_stride +
-                                    (size_t)crow * 128 + 2 * lane);
-#pragma unroll
-                    for (int pj = 0; pj < 2; ++pj)
-#pragma unroll
-                        for (int j = 0; j < G; ++j)
-                            if (pj < np && s0 + j < S) {
-                                out[pj].x += v[pj][j].x;
-                                out[pj].y += v[pj][j].y;
-                            }
-                }
-            };
-            EXL3_GLOBAL __half* outg = gptr(p.out);
-            if (!down) {
-                const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
-                for (int row = wave; row < m; row += nwaves) {
-                    const int crow = crow0 + row;
-                    float2 gu[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
-                    sum_rows(2, crow, gu);
-                    float ga = gu[0].x, gb = gu[0].y, ua = gu[1].x, ub = gu[1].y;
-                    fwht128_pair_fast(ga, gb, lane);
-                    fwht128_pair_fast(ua, ub, lane);
-                    // gate and up outputs in fp16, as the separate linears return them
-                    const __half2 gh =
-                        h2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
-                    const __half2 uh =
-                        h2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
-                    float g0 = __low2float(gh), g1 = __high2float(gh), u0 = __low2float(uh), u1 = __high2float(uh);
-                    if (clamp) {
-                        g0 = fminf(g0, p.limit);
-                        g1 = fminf(g1, p.limit);
-                        u0 = fminf(fmaxf(u0, -p.limit), p.limit);
-                        u1 = fminf(fmaxf(u1, -p.limit), p.limit);
-                    }
-                    const __half2 act = h2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
-                    // input rotation of the down projection for this 128-wide chunk
-                    const __half2 pr = __hmul2(act, ev2);
-                    float da = __low2float(pr), db = __high2float(pr);
-                    fwht128_pair_fast(da, db, lane);
-                    st_h2(outg + (size_t)crow * n + c0, h2_rn(da * kHadNorm, db * kHadNorm));
-                }
-            } else {
-                // fused combine: a row's fixed-point adds are checked only
-                // after the next row's partials have been loaded, so their
-                // round trips overlap
-                FxPair fx{};
-                int ptok = -1, pcnt = 0;
-                for (int row = wave; row < m; row += nwaves) {
-                    const int crow = crow0 + row;
-                    float2 d[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
-                    sum_rows(1, crow, d);
-                    float va = d[0].x, vb = d[0].y;
-                    fwht128_pair_fast(va, vb, lane);
-                    const int entry = direct ? crow : uniform_i(rows_g[crow]);
-                    // the expert's output row in fp16, as the separate linear returns it
-                    const __half2 yh = h2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0));
-                    if (p.fc) {
-                        const int t = entry / p.topk;
-                        const float wv =
-                            p.weights_f16
-                                ? __half2float(__ushort_as_half(
-                                      gptr(reinterpret_cast<const uint16_t*>(p.weights))[entry]))
-                                : gptr(reinterpret_cast<const float*>(p.weights))[entry];
-                        const int c = direct ? direct_valid : uniform_i(gptr(p.tok_valid)[t]);
-                        const FxPair cur =
-                            fx_issue_pair(p.acc + (size_t)t * n + c0, wv * __low2float(yh), wv * __high2float(yh));
-                        if (ptok >= 0)
-                            fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt,
-                                           gptr(p.final_out) + (size_t)ptok * n + c0);
-                        fx = cur;
-                        ptok = t;
-                        pcnt = c;
-                    } else {
-                        st_h2(outg + (size_t)entry * n + c0, yh);
-                    }
-                }
-                if (ptok >= 0)
-                    fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
+                coherent_store(part + idx, v);
             }
         }
+
+        // 5. hand-off: the last of nproj * S arrivals for (unit, column
+        //    block) finishes
+        wait_stores();
+        __syncthreads();
+        int* ctr = p.counters + (size_t)u * nblk_n + bx;
+        if (tid == 0) {
+            // a fused down item has read its h rows (staged above): its first
+            // hand-off also counts it done, in the same round trip, and the
+            // unit's last down item clears the unit's readiness flags for the
+            // next call
+            int dold = 0;
+            if constexpr (wait_h)
+                if (bx == bx0) dold = __hip_atomic_fetch_add(p.done + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            is_last = (old == p.nproj * S - 1);
+            if constexpr (wait_h)
+                if (bx == bx0 && dold == p.dn_items_per_unit - 1) {
+                    for (int j = 0; j < p.ready_nblk; ++j)
+                        __hip_atomic_store(p.ready + (size_t)u * p.ready_stride + j, 0, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(p.done + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+        }
+        __syncthreads();
+        if (!is_last) continue;
+        if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+        // 6. epilogue, one row per wave, 2 columns per lane; split partials
+        //    of a row are all requested before the first add (one round
+        //    trip) and summed in split order
+        auto sum_rows = [&](int np, int crow, float2* out) {
+            constexpr int G = 8;
+            for (int s0 = 0; s0 < S; s0 += G) {
+                float2 v[2][G];
+#pragma unroll
+                for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+                    for (int j = 0; j < G; ++j)
+                        if (pj < np && s0 + j < S)
+                            v[pj][j] = coherent_load2(
+                                p.partials + ((size_t)(bx * p.nproj + pj) * S + s0 + j) * split_stride +
+                                (size_t)crow * 128 + 2 * lane);
+#pragma unroll
+                for (int pj = 0; pj < 2; ++pj)
+#pragma unroll
+                    for (int j = 0; j < G; ++j)
+                        if (pj < np && s0 + j < S) {
+                            out[pj].x += v[pj][j].x;
+                            out[pj].y += v[pj][j].y;
+                        }
+            }
+        };
+        EXL3_GLOBAL __half* outg = gptr(p.out);
+        if (!down) {
+            const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
+            for (int row = wave; row < m; row += nwaves) {
+                const int crow = crow0 + row;
+                float2 gu[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+                sum_rows(2, crow, gu);
+                float ga = gu[0].x, gb = gu[0].y, ua = gu[1].x, ub = gu[1].y;
+                fwht128_pair_fast(ga, gb, lane);
+                fwht128_pair_fast(ua, ub, lane);
+                // gate and up outputs in fp16, as the separate linears return them
+                const __half2 gh =
+                    h2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
+                const __half2 uh =
+                    h2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
+                float g0 = __low2float(gh), g1 = __high2float(gh), u0 = __low2float(uh), u1 = __high2float(uh);
+                if (clamp) {
+                    g0 = fminf(g0, p.limit);
+                    g1 = fminf(g1, p.limit);
+                    u0 = fminf(fmaxf(u0, -p.limit), p.limit);
+                    u1 = fminf(fmaxf(u1, -p.limit), p.limit);
+                }
+                const __half2 act = h2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
+                // input rotation of the down projection for this 128-wide chunk
+                const __half2 pr = __hmul2(act, ev2);
+                float da = __low2float(pr), db = __high2float(pr);
+                fwht128_pair_fast(da, db, lane);
+                if constexpr (FUSED) st_h2_coherent(outg + (size_t)crow * n + c0, h2_rn(da * kHadNorm, db * kHadNorm));
+                else st_h2(outg + (size_t)crow * n + c0, h2_rn(da * kHadNorm, db * kHadNorm));
+            }
+            if constexpr (FUSED) {
+                // the rows of this 128-wide block of h are complete: publish
+                // the block to the down items of the same launch
+                wait_stores();
+                __syncthreads();
+                if (tid == 0)
+                    __hip_atomic_store(p.ready + (size_t)u * p.ready_stride + bx, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else {
+            // fused combine: a row's fixed-point adds are checked only
+            // after the next row's partials have been loaded, so their
+            // round trips overlap
+            FxPair fx{};
+            int ptok = -1, pcnt = 0;
+            for (int row = wave; row < m; row += nwaves) {
+                const int crow = crow0 + row;
+                float2 d[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+                sum_rows(1, crow, d);
+                float va = d[0].x, vb = d[0].y;
+                fwht128_pair_fast(va, vb, lane);
+                const int entry = direct ? crow : uniform_i(rows_g[crow]);
+                // the expert's output row in fp16, as the separate linear returns it
+                const __half2 yh = h2_rn(va * kHadNorm * __low2float(ev0), vb * kHadNorm * __high2float(ev0));
+                if (p.fc) {
+                    const int t = entry / p.topk;
+                    const float wv =
+                        p.weights_f16
+                            ? __half2float(__ushort_as_half(
+                                  gptr(reinterpret_cast<const uint16_t*>(p.weights))[entry]))
+                            : gptr(reinterpret_cast<const float*>(p.weights))[entry];
+                    const int c = direct ? direct_valid : uniform_i(gptr(p.tok_valid)[t]);
+                    const FxPair cur =
+                        fx_issue_pair(p.acc + (size_t)t * n + c0, wv * __low2float(yh), wv * __high2float(yh));
+                    if (ptok >= 0)
+                        fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt,
+                                       gptr(p.final_out) + (size_t)ptok * n + c0);
+                    fx = cur;
+                    ptok = t;
+                    pcnt = c;
+                } else {
+                    st_h2(outg + (size_t)entry * n + c0, yh);
+                }
+            }
+            if (ptok >= 0)
+                fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
+        }
+    }
+}
+
+// Persistent over the work items of one projection pass: the grid is sized
+// to the device, the item count comes from the routing kernel (or the slots
+// of a directly routed token), so no workgroup is launched for an inactive
+// expert.  Items are taken in rounds over the grid, snake order (round r:
+// workgroup b takes item r G + b for even r, r G + G - 1 - b for odd r), so
+// the workgroup with the last (lightest) item of a round takes the first
+// (heaviest) of the next.
+template <int K, int CB, int NS, int MODE, int KW>
+__global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
+    extern __shared__ __align__(16) unsigned char mv_smem[];
+    constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
+    constexpr bool down = MODE == MV_DOWN || MODE == MV_DOWN_DIRECT;
+    const int nunits = direct ? p.topk : uniform_i(gptr(p.rt.counts)[1]);
+    const int per_unit = ((p.n >> 7) / p.bx_per_item) * p.proj_launch * p.splits;
+    const int total = nunits * per_unit;
+    if ((int)blockIdx.x >= total) return;
+    // one token routed directly: its valid slots (the fused combine's count);
+    // with none, workgroup 0 writes the zero output row
+    int direct_valid = 0;
+    if (down && direct) {
+        direct_valid = direct_valid_slots(p);
+        if (direct_valid == 0) {
+            if (blockIdx.x == 0 && p.fc) zero_row(p.final_out, p.n);
+            return;
+        }
+    }
+    const int G = gridDim.x, b0 = blockIdx.x;
+    for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0))
+        moe_item<K, CB, NS, MODE, KW, false>(p, it, mv_smem, direct_valid, rnd == 0);
+}
+
+// One token routed directly, gate/up and down in one persistent launch.
+// Items [0, Ngu) are the gate/up items, [Ngu, Ngu + Ndn) the down items
+// (index order = the order every workgroup takes its items in).  A down item
+// requests its weights at once and then waits (bounded) for the h blocks of
+// its k range, which the gate/up epilogues publish.  Forward progress: the
+// grid is the number of workgroups the device holds at once, so every item
+// has a running workgroup; a workgroup's gate/up items all precede its down
+// items, and gate/up items never wait, so every awaited block is produced.
+template <int K, int CB, int NSG, int NSD>
+__global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(MoeParams pg, MoeParams pd) {
+    extern __shared__ __align__(16) unsigned char mv_smem[];
+    const int direct_valid = direct_valid_slots(pd);
+    if (direct_valid == 0) {
+        if (blockIdx.x == 0 && pd.fc) zero_row(pd.final_out, pd.n);
+        return;
+    }
+    const int ngu = pg.topk * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits;
+    const int total = ngu + pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
+    const int G = gridDim.x, b0 = blockIdx.x;
+    for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0)) {
+        if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true>(pg, it, mv_smem, direct_valid, rnd == 0);
+        else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true>(pd, it - ngu, mv_smem, direct_valid, rnd == 0);
     }
 }
 
@@ -498,13 +638,17 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     const int threads = 256 * p.kw;
     const int mv = p.mode == MOE_DOWN ? (p.direct ? MV_DOWN_DIRECT : MV_DOWN)
                                       : (p.in_rot ? MV_GU_ROT : (p.direct ? MV_GU_DIRECT : MV_GU));
+    // a directly routed token: the item count is known here, so no
+    // workgroup is launched without an item
+    const int direct_items = p.topk * ((p.n >> 7) / p.bx_per_item) * p.proj_launch * p.splits;
 #define EXL3_MV_KW(CBV, NSV, MVV, KWV)                                                                 \
     if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV) {                                          \
         const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV>);       \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe");                                       \
         if (lrc) return lrc;                                                                           \
-        const int grid = moe_grid_size(fn, threads, smem);                                             \
+        int grid = moe_grid_size(fn, threads, smem);                                                   \
         if (grid <= 0) return EXL3_ERR_HIP;                                                            \
+        if (p.direct && grid > direct_items) grid = direct_items;                                      \
         moe_gemv_kernel<K, CBV, NSV, MVV, KWV><<<grid, threads, smem, st>>>(p);                        \
         return launch_status("exl3 moe launch");                                                      \
     }
@@ -523,7 +667,43 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     return EXL3_ERR_UNSUPPORTED;
 }
 
+// Workgroups of the fused one-token kernel that the device holds at once: the
+// smaller of moe_grid_size's estimate and the runtime's occupancy figure
+// (the fused launch relies on every workgroup being resident).
+int moe_fused_grid_size(const void* fn, size_t smem);
+
+// Step counts the fused one-token kernel is instantiated for (per pass).
+inline bool moe_fused_steps_ok(int ns) { return ns == 2 || ns == 4 || ns == 8; }
+
+template <int K>
+int moe_fused_launch_k(int cb, int nsg, int nsd, const MoeParams& pg, const MoeParams& pd, hipStream_t st) {
+    const size_t sg = moe_smem_bytes(4 * nsg, 1), sd = moe_smem_bytes(4 * nsd, 1);
+    const size_t smem = sg > sd ? sg : sd;
+    const int items = pg.topk * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits +
+                      pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
+#define EXL3_MF(CBV, NG, ND)                                                                           \
+    if (cb == CBV && nsg == NG && nsd == ND) {                                                         \
+        const void* fn = reinterpret_cast<const void*>(&moe_fused_direct_kernel<K, CBV, NG, ND>);      \
+        const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe fused");                                 \
+        if (lrc) return lrc;                                                                           \
+        int grid = moe_fused_grid_size(fn, smem);                                                      \
+        if (grid <= 0) return EXL3_ERR_HIP;                                                            \
+        if (grid > items) grid = items;                                                                \
+        moe_fused_direct_kernel<K, CBV, NG, ND><<<grid, 256, smem, st>>>(pg, pd);                      \
+        return launch_status("exl3 moe fused launch");                                                 \
+    }
+#define EXL3_MF_G(CBV, NG) EXL3_MF(CBV, NG, 2) EXL3_MF(CBV, NG, 4) EXL3_MF(CBV, NG, 8)
+#define EXL3_MF_CB(CBV) EXL3_MF_G(CBV, 2) EXL3_MF_G(CBV, 4) EXL3_MF_G(CBV, 8)
+    EXL3_MF_CB(0) EXL3_MF_CB(1) EXL3_MF_CB(2)
+#undef EXL3_MF_CB
+#undef EXL3_MF_G
+#undef EXL3_MF
+    set_error("exl3 moe: no fused kernel for codebook %d steps %d / %d", cb, nsg, nsd);
+    return EXL3_ERR_UNSUPPORTED;
+}
+
 // One instantiation unit per K (exl3_moe_inst.hip built with -DEXL3_K=K).
 int moe_launch(int K, int cb, int ns, const MoeParams& p, hipStream_t st);
+int moe_fused_launch(int K, int cb, int nsg, int nsd, const MoeParams& pg, const MoeParams& pd, hipStream_t st);
 
 }  // namespace exl3

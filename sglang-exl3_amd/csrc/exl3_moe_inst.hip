@@ -13,4 +13,8 @@ namespace exl3 {
 int EXL3_CAT(moe_launch_K, EXL3_K)(int cb, int ns, const MoeParams& p, hipStream_t st) {
     return moe_launch_k<EXL3_K>(cb, ns, p, st);
 }
+int EXL3_CAT(moe_fused_launch_K, EXL3_K)(int cb, int nsg, int nsd, const MoeParams& pg, const MoeParams& pd,
+                                         hipStream_t st) {
+    return moe_fused_launch_k<EXL3_K>(cb, nsg, nsd, pg, pd, st);
+}
 }  // namespace exl3

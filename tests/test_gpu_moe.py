@@ -273,6 +273,78 @@ def test_moe_one_token_direct_routing(topk, E, invalid, fc_tokens, direct, monke
         check_close(o, ex.ref(x, ids, w), f"moe one token direct={direct}")
 
 
+@pytest.mark.parametrize("E,hidden,inter,K,cb,topk,invalid,fc_tokens", [
+    (16, 256, 384, 3, 1, 8, 0, 16),
+    (8, 512, 256, 2, 2, 6, 2, 16),
+    (8, 256, 768, 4, 0, 4, 1, 0),
+    (8, 256, 256, 3, 1, 4, 4, 16),       # no valid slot: zero row
+    (128, 2048, 768, 3, 1, 8, 0, 16),    # headline MoE shape
+    (32, 1024, 1536, 5, 2, 8, 3, 16),
+])
+def test_moe_one_token_fused_launch(E, hidden, inter, K, cb, topk, invalid, fc_tokens, monkeypatch):
+    """One token with one K: gate/up and down in one launch (opt-in, EXL3_MOE_FUSED=1), the down
+    items waiting on readiness flags of the h blocks.  Same bits as the two-launch path
+    (EXL3_MOE_FUSED=0), repeated calls agree (flags and counters are left clear), and against
+    the oracle."""
+    print(f"case: moe fused one token E={E} h={hidden} i={inter} K={K} cb={cb} topk={topk} invalid={invalid} "
+          f"fc_tokens={fc_tokens}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_FC_TOKENS", str(fc_tokens))
+    ex = Experts(E, hidden, inter, (K, K, K), cb, seed=150 + E + K)
+    x = make_x(1, hidden, seed=151 + K)
+    ids, w = _routing(1, topk, E, seed=152 + invalid)
+    ids[0, :invalid] = [-1 if j % 2 else E + j for j in range(invalid)]
+    outs = {}
+    for fused in ("0", "1", "1"):
+        monkeypatch.setenv("EXL3_MOE_FUSED", fused)
+        o = _layer_capi(ex, x, ids, w, cb=cb)
+        torch.cuda.synchronize()
+        if fused in outs:
+            assert torch.equal(o, outs[fused]), "repeated fused call differs"
+        outs[fused] = o
+    assert torch.equal(outs["0"], outs["1"]), "fused launch differs from the two launches"
+    o = outs["1"].float().cpu().numpy()
+    if invalid == topk:
+        assert np.all(o == 0.0)
+    else:
+        check_close(o, ex.ref(x, ids, w), f"moe fused one token E={E}")
+
+
+def test_moe_one_token_fused_graph(monkeypatch):
+    """The fused one-token launch captured in a HIP graph: replays interleaved with eager calls
+    match the eager result, and a routing change between replays is picked up."""
+    monkeypatch.setenv("EXL3_MOE_FUSED", "1")
+    E, hidden, inter, topk = 32, 512, 768, 8
+    ex = Experts(E, hidden, inter, (3, 3, 3), 1, seed=160)
+    x = make_x(1, hidden, seed=161)
+    ids, w = _routing(1, topk, E, seed=162)
+    xd, idd, wd = (torch.from_numpy(a).cuda() for a in (x, ids, w))
+    a = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gout = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, a), f"graph replay {r} differs from eager"
+        ex.layer(xd, idd, wd)
+        torch.cuda.synchronize()
+    ids2, w2 = _routing(1, topk, E, seed=163)
+    ids2[0, 3] = -1
+    idd.copy_(torch.from_numpy(ids2))
+    wd.copy_(torch.from_numpy(w2))
+    g.replay()
+    torch.cuda.synchronize()
+    check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe fused graph new routing")
+
+
 @pytest.mark.parametrize("T,inter,fc_tokens", [(20, 768, 100), (20, 1536, 0), (3, 768, 16)])
 def test_moe_down_twelve_step_items(T, inter, fc_tokens, monkeypatch):
     """Down pass with 12-step items (48 k-slices: one split at inter 768, two at 1536), forced
