@@ -169,18 +169,6 @@ __device__ __forceinline__ void wait_ready(const int* f, int j0, int j1, int nsl
     }
 }
 
-// Weight steps a MoE work item keeps in flight: every step of the item up to
-// `words` words per lane (24 for a directly routed token, 12 for the routed
-// down pass, two steps for the routed gate/up passes, whose multi-row code
-// spills beyond that).  A small pass has about one item per workgroup and its
-// weight stream is latency-bound, so the bytes in flight set its rate.
-template <int K, int NS, int MODE>
-__host__ __device__ constexpr int moe_depth() {
-    constexpr int words = (MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT) ? 24 : MODE == MV_DOWN ? 12 : 2 * K;
-    constexpr int budget = words / K > 2 ? words / K : 2;
-    return NS < budget ? NS : budget;
-}
-
 // Valid slots of a directly routed token (ids in [0, E)).
 __device__ __forceinline__ int direct_valid_slots(const MoeParams& p) {
     int v = 0;
@@ -313,7 +301,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
             }
         }
     };
-    uint32_t w[moe_depth<K, NS, MODE>()][K];
+    uint32_t w[gv_depth<K>()][K];
     if constexpr (wait_h) {
         if (!p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
         if (tid == 0)

@@ -26,7 +26,7 @@ from .base import LinearMethodBase, set_weight_attrs
 
 logger = logging.getLogger("sglang.exl3")
 
-__all__ = ["EXL3DenseLinear", "EXL3LinearMethod", "linear_forward"]
+__all__ = ["EXL3DenseLinear", "EXL3LinearMethod", "linear_forward", "_mgemm_two", "_mgemm_pair_compatible"]
 
 # Rows up to which two shards sharing one input run as one batched GEMV launch.
 FUSED_PAIR_MAX_ROWS = 64
@@ -114,12 +114,49 @@ def _pair_tables(layer, a: EXL3DenseLinear, b: EXL3DenseLinear, dev: torch.devic
     return cache[key]
 
 
-def fused_pair(layer, x2: torch.Tensor, a: EXL3DenseLinear, b: EXL3DenseLinear):
-    """Both linears on one shared fp16 input in one launch (exl3_p2b_gemv_batched)."""
+def fused_pair(layer, x2: torch.Tensor, a: EXL3DenseLinear, b: EXL3DenseLinear,
+               x2_b: Optional[torch.Tensor] = None):
+    """Both linears in one launch (exl3_p2b_gemv_batched): on the shared fp16
+    input x2, or a on x2 and b on x2_b (the batched kernel's per-expert input)."""
     t = _pair_tables(layer, a, b, x2.device)
-    y = torch.ops.sglang_exl3.p2b_gemv_batched(x2, t["trellis"], t["suh"], t["svh"], t["ids"], a.K, a.mcg,
+    xv = x2 if x2_b is None or x2_b is x2 else torch.stack((x2, x2_b), dim=0)
+    y = torch.ops.sglang_exl3.p2b_gemv_batched(xv, t["trellis"], t["suh"], t["svh"], t["ids"], a.K, a.mcg,
                                                a.out_features)
     return y[0], y[1]
+
+
+def _mgemm_pair_compatible(lin0: Optional[EXL3DenseLinear], lin1: Optional[EXL3DenseLinear]) -> bool:
+    """Whether two linears run as one batched launch: same K, input and output
+    widths and codebook, MCG or mul1 (reference: src/sglang_exl3/dense.py:61-70)."""
+    return _pair_compatible(lin0, lin1)
+
+
+def _mgemm_two(layer, x2: torch.Tensor, lin0: EXL3DenseLinear, lin1: EXL3DenseLinear,
+               x2_b: Optional[torch.Tensor] = None):
+    """(x2 @ W0, x2_b @ W1) for two EXL3 linears; x2_b None (or x2 itself)
+    means both read x2 (reference: src/sglang_exl3/dense.py:89-117, called for
+    (q, g) and for (k, v) under a value residual in
+    src/sglang_exl3/models/ricursive.py:261-281).  A compatible pair of up to
+    FUSED_PAIR_MAX_ROWS rows runs as one batched launch; any other pair
+    (different widths, K or codebook, or more rows) as two launches.  The
+    outputs are fp16 [rows, out_f] and freshly allocated on every call."""
+    if x2.dim() != 2:
+        raise ValueError(f"_mgemm_two: x2 must be [rows, in_features], got {tuple(x2.shape)}")
+    same = x2_b is None or x2_b is x2
+    other = x2 if same else x2_b
+    if other.dim() != 2 or other.shape[0] != x2.shape[0] or other.shape[1] != lin1.in_features \
+            or x2.shape[1] != lin0.in_features:
+        raise ValueError(f"_mgemm_two: inputs {tuple(x2.shape)} / {tuple(other.shape)} do not fit linears of "
+                         f"{lin0.in_features} / {lin1.in_features} inputs")
+
+    def f16(t):
+        return t if t.dtype == torch.float16 and t.is_contiguous() else t.to(torch.float16).contiguous()
+
+    x2 = f16(x2)
+    other = x2 if same else f16(other)
+    if x2.shape[0] <= FUSED_PAIR_MAX_ROWS and _pair_compatible(lin0, lin1):
+        return fused_pair(layer, x2, lin0, lin1, None if same else other)
+    return lin0.forward(x2), lin1.forward(other)
 
 
 class EXL3LinearMethod(LinearMethodBase):

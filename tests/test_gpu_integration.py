@@ -169,3 +169,78 @@ def test_moe_method_prefill_batch_stays_native():
     assert layer._exl3_last_apply == "native"
     sel = np.sort(rng.choice(T, 48, replace=False))
     check_close(out.float().cpu().numpy()[sel], oracle.moe_ref(x[sel], ids[sel], w[sel], experts), "moe prefill method")
+
+
+@pytest.mark.parametrize("rows", [1, 5, 80])
+def test_checkpoint_to_forward(tmp_path, rows):
+    """A two-shard safetensors checkpoint streamed (iter_safetensors_pread) and routed
+    (route_exl3_sidecar: fused qkv group cut into q/k/v shards, gate/up merged) into
+    EXL3LinearMethod layers on the device; each layer's apply() against the oracle on the
+    checkpoint's own groups."""
+    from test_loader_sidecar import build_checkpoint, load_layers
+
+    files, groups, dims = build_checkpoint(tmp_path)
+    layers, leftovers = load_layers(files, dims)
+    assert leftovers == ["model.norm.weight"]
+    cfg = EXL3Config.from_config({"bits": 3, "codebook": "mcg"})
+
+    def ref(x, mods):
+        outs = []
+        for mod in mods:
+            t, su, sv = (a.numpy() for a in groups[mod])
+            outs.append(oracle.matmul(x, oracle.dequant(t.view(np.int16), su, sv, 3, 1, rtz=True)))
+        return np.concatenate(outs, axis=1)
+
+    cases = {
+        "model.layers.0.self_attn.qkv_proj": ["model.layers.0.self_attn.qkv_proj"],
+        "model.layers.0.self_attn.o_proj": ["model.layers.0.self_attn.o_proj"],
+        "model.layers.0.mlp.gate_up_proj": ["model.layers.0.mlp.gate_proj", "model.layers.0.mlp.up_proj"],
+    }
+    for prefix, mods in cases.items():
+        layer = layers[prefix]
+        method = EXL3LinearMethod(cfg, bits=3)
+        method.process_weights_after_loading(layer)
+        assert all(lin.trellis.is_cuda for lin in layer._exl3_linears)
+        k = layer._exl3_lin_input_size_per_partition
+        x = make_x(rows, k, seed=rows + len(prefix))
+        y = method.apply(layer, torch.from_numpy(x).cuda().to(torch.bfloat16))
+        torch.cuda.synchronize()
+        assert y.dtype == torch.float16  # the layer's params dtype
+        xr = torch.from_numpy(x).to(torch.bfloat16).to(torch.float16).numpy()
+        check_close(y.float().cpu().numpy(), ref(xr, mods), f"checkpoint {prefix} rows={rows}")
+
+
+@pytest.mark.parametrize("rows,n0,n1,K0,K1,cb0,cb1,second", [
+    (1, 256, 256, 3, 3, 1, 1, False),     # (q, g): one batched launch on a shared input
+    (4, 384, 384, 4, 4, 2, 2, True),      # (k, v) with a value residual: per-linear inputs, one launch
+    (8, 256, 128, 3, 3, 1, 1, True),      # unequal widths: two launches
+    (2, 256, 256, 3, 2, 1, 1, False),     # different K: two launches
+    (3, 256, 256, 3, 3, 1, 2, True),      # different codebooks: two launches
+    (80, 256, 256, 3, 3, 2, 2, True),     # above the batched row limit: two launches
+])
+def test_mgemm_two(rows, n0, n1, K0, K1, cb0, cb1, second):
+    """_mgemm_two (reference dense.py:89-117): (x @ W0, x_b @ W1) against the oracle."""
+    from sglang_exl3.dense import _mgemm_pair_compatible, _mgemm_two
+
+    k = 256
+    w0, w1 = _scaled(k, n0, K0, seed=40 + rows), _scaled(k, n1, K1, seed=41 + rows)
+    mk = {1: torch.tensor([1], dtype=torch.int32), 2: None}
+    mu = {1: None, 2: torch.tensor([1], dtype=torch.int32)}
+    lins = [EXL3DenseLinear(*(torch.from_numpy(a).cuda() for a in w), mcg=mk[cb], mul1=mu[cb])
+            for w, cb in ((w0, cb0), (w1, cb1))]
+    assert _mgemm_pair_compatible(*lins) == (n0 == n1 and K0 == K1 and cb0 == cb1)
+    x = make_x(rows, k, seed=50 + rows)
+    xb = make_x(rows, k, seed=60 + rows) if second else None
+    layer = nn.Module()
+    y0, y1 = _mgemm_two(layer, torch.from_numpy(x).cuda(), *lins,
+                        x2_b=None if xb is None else torch.from_numpy(xb).cuda())
+    torch.cuda.synchronize()
+    assert y0.shape == (rows, n0) and y1.shape == (rows, n1) and y0.dtype == y1.dtype == torch.float16
+    ref0 = oracle.matmul(x, oracle.dequant(*w0, K0, cb0, rtz=True))
+    ref1 = oracle.matmul(x if xb is None else xb, oracle.dequant(*w1, K1, cb1, rtz=True))
+    check_close(y0.float().cpu().numpy(), ref0, f"mgemm first rows={rows}")
+    check_close(y1.float().cpu().numpy(), ref1, f"mgemm second rows={rows}")
+    # fresh outputs on every call
+    z0, _ = _mgemm_two(layer, torch.from_numpy(x).cuda(), *lins,
+                       x2_b=None if xb is None else torch.from_numpy(xb).cuda())
+    assert z0.data_ptr() != y0.data_ptr() and torch.equal(z0, y0)
