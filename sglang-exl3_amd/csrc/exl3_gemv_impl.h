@@ -110,6 +110,31 @@ __device__ __forceinline__ float sum_splits(const float* p, size_t stride, int S
     return sum;
 }
 
+// Two adjacent columns of sum_splits (64-bit loads), for `np` projections at
+// once (pointer p[j], j < np), in groups of 8 splits: one round trip for up
+// to 8 splits with at most 2 * 8 * np values in flight.
+template <int NP>
+__device__ __forceinline__ void sum_splits2(const float* const (&p)[NP], size_t stride, int S, float2 (&out)[NP]) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) out[j] = make_float2(0.f, 0.f);
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        float2 v[NP][8];
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                v[j][t] = (s0 + t < S) ? coherent_load2(p[j] + (size_t)(s0 + t) * stride) : make_float2(0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                if (s0 + t < S) {
+                    out[j].x += v[j][t].x;
+                    out[j].y += v[j][t].y;
+                }
+    }
+}
+
 // ------------------------------------------- fixed-point output accumulators
 //
 // Partial sums of one output element from several workgroups meet in a 64-bit
@@ -291,7 +316,9 @@ __device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[D][K], const EXL
     }
 }
 
-template <int K, int CB, int MB, int NS>
+// GU: the gate/up SwiGLU mode (p.gu), a separate instance so that the plain
+// GEMV carries none of its registers (71 against 199 VGPRs at K=4).
+template <int K, int CB, int MB, int NS, bool GU>
 __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     constexpr int D = gv_depth<K>();
     extern __shared__ __align__(16) unsigned char gv_smem[];
@@ -305,7 +332,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         trellis = reinterpret_cast<const uint32_t*>(gptr(p.t_tab)[id]);
         suh = reinterpret_cast<const __half*>(gptr(p.su_tab)[id]);
         svh = reinterpret_cast<const __half*>(gptr(p.sv_tab)[id]);
-    } else if (p.gu && e) {
+    } else if (GU && e) {
         trellis = p.trellis2;
         suh = p.suh2;
         svh = p.svh2;
@@ -437,7 +464,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     // hand-off needs only "my stores completed" before the counter increment;
     // no L2 write-back or invalidate.
     const int nblk_n = n >> 7;
-    if (p.splits > 1 || p.gu) {
+    if (p.splits > 1 || GU) {
         const size_t cblk = (size_t)e * nblk_n + bx;
         float* part = p.partials + (cblk * p.splits + sidx) * (size_t)m * 128;
         for (int idx = tid; idx < m * 128; idx += nthreads) coherent_store(part + idx, ybuf[idx]);
@@ -445,15 +472,15 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         __syncthreads();
         __shared__ int is_last;
         // gate/up mode: one counter per column block for both projections
-        const size_t ctr = p.gu ? (size_t)bx : cblk;
-        const int arrivals = p.gu ? 2 * p.splits : p.splits;
+        const size_t ctr = GU ? (size_t)bx : cblk;
+        const int arrivals = GU ? 2 * p.splits : p.splits;
         if (tid == 0) {
             const int old = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             is_last = (old == arrivals - 1);
         }
         __syncthreads();
         if (!is_last) return;
-        if (p.gu) {
+        if constexpr (GU) {
             // gate and up of each row: split sums (one round trip each), output
             // rotation, norm and svh of both, then the SwiGLU
             if (tid == 0) __hip_atomic_store(p.counters + ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -465,10 +492,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
             const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
             EXL3_GLOBAL __half* yg = gptr(p.y);
             for (int row = wave; row < m; row += nwaves) {
-                float ga = sum_splits(pg + row * 128 + 2 * lane, rstride, p.splits);
-                float gb = sum_splits(pg + row * 128 + 2 * lane + 1, rstride, p.splits);
-                float ua = sum_splits(pu + row * 128 + 2 * lane, rstride, p.splits);
-                float ub = sum_splits(pu + row * 128 + 2 * lane + 1, rstride, p.splits);
+                const float* const src[2] = {pg + row * 128 + 2 * lane, pu + row * 128 + 2 * lane};
+                float2 gu2[2];
+                sum_splits2<2>(src, rstride, p.splits, gu2);
+                float ga = gu2[0].x, gb = gu2[0].y, ua = gu2[1].x, ub = gu2[1].y;
                 fwht128_pair_fast(ga, gb, lane);
                 fwht128_pair_fast(ua, ub, lane);
                 ga = ga * kHadNorm * __low2float(svg);
@@ -514,14 +541,16 @@ int gemv_launch_k(int cb, int mb, const GemvParams& p, int experts, hipStream_t 
     dim3 grid(p.n / 128, p.splits, experts);
     const size_t smem = gemv_smem_bytes(p.m, 4 * p.nsteps * p.kw, p.kw);
     const int threads = 256 * p.kw;
-#define EXL3_GV_NS(CBV, MBV, NSV)                                                                      \
-    if (cb == CBV && mb == MBV && p.nsteps == NSV) {                                                   \
-        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV>);                \
+#define EXL3_GV_GU(CBV, MBV, NSV, GUV)                                                                 \
+    if (cb == CBV && mb == MBV && p.nsteps == NSV && (p.gu != 0) == GUV) {                             \
+        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV, GUV>);           \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 gemv");                                      \
         if (lrc) return lrc;                                                                           \
-        gemv_kernel<K, CBV, MBV, NSV><<<grid, threads, smem, st>>>(p);                                 \
+        gemv_kernel<K, CBV, MBV, NSV, GUV><<<grid, threads, smem, st>>>(p);                            \
         return launch_status("exl3 gemv launch");                                                      \
     }
+// gate/up mode runs with one row block (m <= 4)
+#define EXL3_GV_NS(CBV, MBV, NSV) EXL3_GV_GU(CBV, MBV, NSV, false) if constexpr (MBV == 1) EXL3_GV_GU(CBV, MBV, NSV, true)
 #define EXL3_GV_CASE(CBV, MBV) \
     EXL3_GV_NS(CBV, MBV, 2) EXL3_GV_NS(CBV, MBV, 4) EXL3_GV_NS(CBV, MBV, 8) EXL3_GV_NS(CBV, MBV, 16)
     EXL3_GV_CASE(0, 1) EXL3_GV_CASE(0, 2) EXL3_GV_CASE(0, 4)
@@ -529,6 +558,7 @@ int gemv_launch_k(int cb, int mb, const GemvParams& p, int experts, hipStream_t 
     EXL3_GV_CASE(2, 1) EXL3_GV_CASE(2, 2) EXL3_GV_CASE(2, 4)
 #undef EXL3_GV_CASE
 #undef EXL3_GV_NS
+#undef EXL3_GV_GU
     set_error("exl3 gemv: no kernel for codebook %d row blocks %d steps %d", cb, mb, p.nsteps);
     return EXL3_ERR_UNSUPPORTED;
 }

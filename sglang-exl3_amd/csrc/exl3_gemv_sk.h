@@ -28,6 +28,9 @@
 namespace exl3 {
 
 constexpr int SK_THREADS = 256;
+#ifndef EXL3_SK_DEPTH_WORDS
+#define EXL3_SK_DEPTH_WORDS 8
+#endif
 
 struct GemvSkParams {
     const __half* x;          // [m][k]
@@ -72,9 +75,16 @@ __device__ __forceinline__ void sk_frags(const uint32_t* buf, const uint32_t* mi
     (sk_frag<K, CB, Fs>(buf, mid, A, acc), ...);
 }
 
+// Weight steps in flight per wave: the whole piece when its words fit
+// EXL3_SK_DEPTH_WORDS registers per lane, else two.
+template <int K, int NS>
+__host__ __device__ constexpr int sk_depth() {
+    return NS * K <= EXL3_SK_DEPTH_WORDS ? NS : (gv_depth<K>() < NS ? gv_depth<K>() : NS);
+}
+
 template <int K, int CB, int NS, int MR>
 __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
-    constexpr int D = gv_depth<K>();
+    constexpr int D = sk_depth<K, NS>();
     extern __shared__ __align__(16) unsigned char sk_smem[];
 
     const int n = p.n, P = p.pieces, m = p.m, k = p.k;
