@@ -26,6 +26,13 @@
 
 namespace exl3 {
 
+// Wave priority 1 over the MFMA phase of the wide-tile kernel, so the matrix
+// core is fed first while the co-resident workgroup decodes (config 3, M=2048:
+// 552 -> 545 us).  Build with -DEXL3_FAT_SETPRIO=0 to leave priorities alone.
+#ifndef EXL3_FAT_SETPRIO
+#define EXL3_FAT_SETPRIO 1
+#endif
+
 constexpr int FAT_THREADS = 256;  // 4 waves x 32 output columns
 constexpr int FAT_CH = 4;         // steps per staged A chunk (256 k)
 constexpr int FAT_ROWB = FAT_CH * 4 * 2 * 16 + 16;  // bytes per staged A row (+16: bank spread)
@@ -518,7 +525,9 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
         load_step(n2);
         load_a(n1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EXL3_FAT_SETPRIO) __builtin_amdgcn_s_setprio(1);
         mfma_phase(slot_c);
+        if constexpr (EXL3_FAT_SETPRIO) __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         write_a(SL ^ 1);
         // A barrier on the LDS traffic only (__syncthreads would also wait for
