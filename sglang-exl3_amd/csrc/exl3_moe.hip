@@ -611,6 +611,10 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.weights = weights;
     p.weights_f16 = weights_f16;
     p.final_out = reinterpret_cast<__half*>(out);
+    // the fused combine one round trip per split (each split adds its rotated
+    // partial rows into the output accumulators) when every token's count of
+    // contributions (valid slots x splits) fits the accumulators' count bits
+    p.fxs = L.fc && L.dn.kw == 1 && topk * L.dn.splits <= SK_MAX_CONTRIB && env_int("EXL3_MOE_FXS", 1) != 0;
     if (fused) {
         p.counters = reinterpret_cast<int*>(w8) + (size_t)topk * (inter / 128);
         p.partials = reinterpret_cast<float*>(w8 + L.part_dn_off);

@@ -120,6 +120,12 @@ struct MoeParams {
     int poll_sleep;    // s_sleep(8) calls between two polls
     int prime_late;    // down items request their weights after the wait
     int dn_items_per_unit;
+    // Down pass with the fused combine, one round trip per split (fxs != 0,
+    // moe_gemv_kernel<.., FXS = true>): each k-split item rotates and scales
+    // its own partial rows and adds w * svh * H(partial) / sqrt(128) straight
+    // into the token's fixed-point accumulators, which complete after
+    // valid-slots x splits contributions (the output rotation is linear).
+    int fxs;
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
@@ -193,7 +199,7 @@ __device__ __forceinline__ void zero_row(__half* out, int n) {
 // the LDS of a previous one).  FUSED: the gate/up and down passes share one
 // launch (moe_fused_direct_kernel): gate/up epilogues publish each finished
 // 128-wide block of h, and down items wait for the blocks they read.
-template <int K, int CB, int NS, int MODE, int KW, bool FUSED>
+template <int K, int CB, int NS, int MODE, int KW, bool FUSED, bool FXS = false>
 __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned char* mv_smem, int direct_valid,
                                          bool first) {
     constexpr int ROWS = MOE_UNIT_ROWS;
@@ -376,6 +382,51 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         acc[0][0] = float4_t{0.f, 0.f, 0.f, 0.f};
         acc[0][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         decode_mfma_steps<K, CB, 1, NS>(w, tiles(bx), step_stride, a_base, a_live, acc);
+
+        if constexpr (FXS) {
+            static_assert(KW == 1 && (MODE == MV_DOWN || MODE == MV_DOWN_DIRECT), "split fixed-point adds: down pass");
+            // the four waves' column slices of the unit's rows meet in LDS
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 4 * g + r;
+                if (row >= m) continue;
+#pragma unroll
+                for (int c = 0; c < 2; ++c) ybuf[row * 128 + cw * 32 + (i >> 3) * 16 + (i & 7) + 8 * c] = acc[0][c][r];
+            }
+            __syncthreads();
+            // one row per wave: mul1 map, output rotation, svh, routing
+            // weight, then the adds; a row's adds are checked after the next
+            // row's have been issued, so their round trips overlap
+            FxPair fx{};
+            int ptok = -1, pcnt = 0;
+            for (int row = wave; row < m; row += nwaves) {
+                float va = ybuf[row * 128 + 2 * lane], vb = ybuf[row * 128 + 2 * lane + 1];
+                if constexpr (CB == 2) {
+                    float sx = 0.f;
+                    for (int bb = 0; bb < nblk128; ++bb) sx += xsum[row * nblk128 + bb];
+                    va = va * kMul1Kinv + kMul1Delta * sx;
+                    vb = vb * kMul1Kinv + kMul1Delta * sx;
+                }
+                fwht128_pair_fast(va, vb, lane);
+                const int crow = crow0 + row;
+                const int entry = direct ? crow : uniform_i(rows_g[crow]);
+                const int t = entry / p.topk;
+                const float wv = p.weights_f16
+                                     ? __half2float(__ushort_as_half(gptr(reinterpret_cast<const uint16_t*>(p.weights))[entry]))
+                                     : gptr(reinterpret_cast<const float*>(p.weights))[entry];
+                const int c = (direct ? direct_valid : uniform_i(gptr(p.tok_valid)[t])) * S;
+                const float sa = wv * kHadNorm * __low2float(ev0), sb = wv * kHadNorm * __high2float(ev0);
+                const FxPair cur = fx_issue_pair(p.acc + (size_t)t * n + c0, va * sa, vb * sb);
+                if (ptok >= 0)
+                    fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
+                fx = cur;
+                ptok = t;
+                pcnt = c;
+            }
+            if (ptok >= 0)
+                fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
+            continue;
+        }
 
         // 4. k waves summed through LDS, mul1 affine map, partial rows out
         //    (one k wave: straight from the accumulators, no LDS tile, so
@@ -561,7 +612,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
 // workgroup b takes item r G + b for even r, r G + G - 1 - b for odd r), so
 // the workgroup with the last (lightest) item of a round takes the first
 // (heaviest) of the next.
-template <int K, int CB, int NS, int MODE, int KW>
+template <int K, int CB, int NS, int MODE, int KW, bool FXS = false>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
     extern __shared__ __align__(16) unsigned char mv_smem[];
     constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
@@ -582,7 +633,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     }
     const int G = gridDim.x, b0 = blockIdx.x;
     for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0))
-        moe_item<K, CB, NS, MODE, KW, false>(p, it, mv_smem, direct_valid, rnd == 0);
+        moe_item<K, CB, NS, MODE, KW, false, FXS>(p, it, mv_smem, direct_valid, rnd == 0);
 }
 
 // One token routed directly, gate/up and down in one persistent launch.
@@ -611,10 +662,13 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
 }
 
 // Dynamic LDS bytes of moe_gemv_kernel.
-inline size_t moe_smem_bytes(int kts_wg, int kw) {
+// fxs: the split fixed-point down pass, whose one k-wave still meets in an
+// LDS tile of the unit's rows.
+inline size_t moe_smem_bytes(int kts_wg, int kw, bool fxs = false) {
     const int rows = MOE_UNIT_ROWS;
     const size_t xs = ((size_t)kts_wg * 4 * rows * 8 * 2 + 16 + 15) & ~(size_t)15;
-    return xs + (size_t)((rows * (kts_wg / 8) + 3) & ~3) * 4 + (kw > 1 ? (size_t)kw * rows * 128 * 4 : 0);
+    const size_t tile = kw > 1 ? (size_t)kw * rows * 128 * 4 : (fxs ? (size_t)rows * 128 * 4 : 0);
+    return xs + (size_t)((rows * (kts_wg / 8) + 3) & ~3) * 4 + tile;
 }
 
 // Workgroups of moe_gemv_kernel<...> the device holds at once (cached).
@@ -622,28 +676,31 @@ int moe_grid_size(const void* fn, int threads, size_t smem);
 
 template <int K>
 int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
-    const size_t smem = moe_smem_bytes(4 * ns * p.kw, p.kw);
+    const bool fxs = p.fxs && p.mode == MOE_DOWN && p.kw == 1;
+    const size_t smem = moe_smem_bytes(4 * ns * p.kw, p.kw, fxs);
     const int threads = 256 * p.kw;
     const int mv = p.mode == MOE_DOWN ? (p.direct ? MV_DOWN_DIRECT : MV_DOWN)
                                       : (p.in_rot ? MV_GU_ROT : (p.direct ? MV_GU_DIRECT : MV_GU));
     // a directly routed token: the item count is known here, so no
     // workgroup is launched without an item
     const int direct_items = p.topk * ((p.n >> 7) / p.bx_per_item) * p.proj_launch * p.splits;
-#define EXL3_MV_KW(CBV, NSV, MVV, KWV)                                                                 \
-    if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV) {                                          \
-        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV>);       \
+#define EXL3_MV_F(CBV, NSV, MVV, KWV, FXV)                                                             \
+    if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV && fxs == FXV) {                            \
+        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV, FXV>);  \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe");                                       \
         if (lrc) return lrc;                                                                           \
         int grid = moe_grid_size(fn, threads, smem);                                                   \
         if (grid <= 0) return EXL3_ERR_HIP;                                                            \
         if (p.direct && grid > direct_items) grid = direct_items;                                      \
-        moe_gemv_kernel<K, CBV, NSV, MVV, KWV><<<grid, threads, smem, st>>>(p);                        \
+        moe_gemv_kernel<K, CBV, NSV, MVV, KWV, FXV><<<grid, threads, smem, st>>>(p);                   \
         return launch_status("exl3 moe launch");                                                      \
     }
+#define EXL3_MV_KW(CBV, NSV, MVV, KWV) EXL3_MV_F(CBV, NSV, MVV, KWV, false)
 #define EXL3_MV_NS(CBV, NSV, MVV) EXL3_MV_KW(CBV, NSV, MVV, 1) EXL3_MV_KW(CBV, NSV, MVV, 2)
 #define EXL3_MV_MODES(CBV, NSV)                                                                        \
     EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)             \
-    EXL3_MV_KW(CBV, NSV, MV_GU_DIRECT, 1) EXL3_MV_KW(CBV, NSV, MV_DOWN_DIRECT, 1)
+    EXL3_MV_KW(CBV, NSV, MV_GU_DIRECT, 1) EXL3_MV_KW(CBV, NSV, MV_DOWN_DIRECT, 1)                        \
+    EXL3_MV_F(CBV, NSV, MV_DOWN, 1, true) EXL3_MV_F(CBV, NSV, MV_DOWN_DIRECT, 1, true)
 #define EXL3_MV_CASE(CBV) \
     EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 12) EXL3_MV_MODES(CBV, 16)
     EXL3_MV_CASE(0) EXL3_MV_CASE(1) EXL3_MV_CASE(2)
@@ -651,6 +708,7 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
 #undef EXL3_MV_MODES
 #undef EXL3_MV_NS
 #undef EXL3_MV_KW
+#undef EXL3_MV_F
     set_error("exl3 moe: no kernel for codebook %d steps %d k waves %d", cb, ns, p.kw);
     return EXL3_ERR_UNSUPPORTED;
 }

@@ -283,12 +283,13 @@ def test_moe_one_token_direct_routing(topk, E, invalid, fc_tokens, direct, monke
 ])
 def test_moe_one_token_fused_launch(E, hidden, inter, K, cb, topk, invalid, fc_tokens, monkeypatch):
     """One token with one K: gate/up and down in one launch (opt-in, EXL3_MOE_FUSED=1), the down
-    items waiting on readiness flags of the h blocks.  Same bits as the two-launch path
-    (EXL3_MOE_FUSED=0), repeated calls agree (flags and counters are left clear), and against
-    the oracle."""
+    items waiting on readiness flags of the h blocks.  Same bits as the two-launch path with the
+    same per-block hand-off (EXL3_MOE_FUSED=0, EXL3_MOE_FXS=0), repeated calls agree (flags and
+    counters are left clear), and against the oracle."""
     print(f"case: moe fused one token E={E} h={hidden} i={inter} K={K} cb={cb} topk={topk} invalid={invalid} "
           f"fc_tokens={fc_tokens}", flush=True)
     monkeypatch.setenv("EXL3_MOE_FC_TOKENS", str(fc_tokens))
+    monkeypatch.setenv("EXL3_MOE_FXS", "0")  # the two launches with the fused launch's per-block hand-off
     ex = Experts(E, hidden, inter, (K, K, K), cb, seed=150 + E + K)
     x = make_x(1, hidden, seed=151 + K)
     ids, w = _routing(1, topk, E, seed=152 + invalid)
@@ -343,6 +344,36 @@ def test_moe_one_token_fused_graph(monkeypatch):
     g.replay()
     torch.cuda.synchronize()
     check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe fused graph new routing")
+
+
+@pytest.mark.parametrize("T,topk,E,hidden,inter,K,cb,invalid", [
+    (1, 8, 16, 256, 768, 3, 1, 0), (1, 6, 8, 512, 384, 4, 2, 2), (5, 4, 8, 256, 1536, 3, 0, 3),
+    (16, 8, 32, 512, 768, 2, 1, 4), (12, 2, 4, 256, 256, 5, 2, 0),
+])
+def test_moe_split_fixed_point_combine(T, topk, E, hidden, inter, K, cb, invalid, monkeypatch):
+    """Fused combine with one round trip per split (EXL3_MOE_FXS, default on): every k-split item
+    adds its rotated, scaled partial rows into the output accumulators.  Against the oracle, against
+    the per-column-block hand-off (EXL3_MOE_FXS=0) within the same bar, repeated calls bit-identical,
+    a token without valid slots a zero row."""
+    print(f"case: moe split fixed-point T={T} topk={topk} E={E} h={hidden} i={inter} K={K} cb={cb}", flush=True)
+    ex = Experts(E, hidden, inter, (K, K, K), cb, seed=170 + T + K)
+    x = make_x(T, hidden, seed=171 + T)
+    ids, w = _routing(T, topk, E, seed=172 + T, invalid=invalid)
+    if T > 2:
+        ids[T // 2, :] = -1
+    monkeypatch.setenv("EXL3_MOE_FXS", "0")
+    base = _layer_capi(ex, x, ids, w, cb=cb)
+    monkeypatch.setenv("EXL3_MOE_FXS", "1")
+    a = _layer_capi(ex, x, ids, w, cb=cb)
+    b = _layer_capi(ex, x, ids, w, cb=cb)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    o = a.float().cpu().numpy()
+    if T > 2:
+        assert np.all(o[T // 2] == 0.0)
+    ref = ex.ref(x, ids, w)
+    check_close(o, ref, f"moe split fixed-point T={T}")
+    check_close(o, base.float().cpu().numpy(), f"moe split fixed-point vs hand-off T={T}")
 
 
 @pytest.mark.parametrize("T,inter,fc_tokens", [(20, 768, 100), (20, 1536, 0), (3, 768, 16)])
