@@ -322,27 +322,28 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
 
     // 2. stage the rows in A-fragment order once for all column blocks of
     //    the item (rotated here unless they arrive rotated)
+    // values kk and kk + 1 of a lane sit at xs_index(kk) and xs_index(kk) + 2
+    // (8-byte aligned), so (a, a, c, c) is one 64-bit LDS store
     auto stage = [&](int b, __half2 xv, __half2 sv) {
         const int row = b / nblk128, bb = b - row * nblk128;
         const int kk = bb * 128 + 2 * lane;
-        _Float16 ha, hc;
+        uint32_t bits;
         if (pre_rotated) {
-            ha = (_Float16)__low2float(xv);
-            hc = (_Float16)__high2float(xv);
+            bits = *reinterpret_cast<const uint32_t*>(&xv);
         } else {
             const __half2 pr = __hmul2(xv, sv);
             float fa = __low2float(pr), fc = __high2float(pr);
             fwht128_pair_fast(fa, fc, lane);
-            ha = f16_rn(fa * kHadNorm);
-            hc = f16_rn(fc * kHadNorm);
+            const _Float16 ha = f16_rn(fa * kHadNorm), hc = f16_rn(fc * kHadNorm);
+            bits = (uint32_t)__builtin_bit_cast(unsigned short, ha) |
+                   ((uint32_t)__builtin_bit_cast(unsigned short, hc) << 16);
         }
-        const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
-        xs[ia] = ha;
-        xs[ia + 1] = ha;
-        xs[ic] = hc;
-        xs[ic + 1] = hc;
+        const uint32_t da = __builtin_amdgcn_perm(bits, bits, 0x01000100u);  // (a, a)
+        const uint32_t dc = __builtin_amdgcn_perm(bits, bits, 0x03020302u);  // (c, c)
+        *reinterpret_cast<uint2*>(xs + xs_index(kk, row, kts_wg)) = make_uint2(da, dc);
         if constexpr (CB == 2) {
-            const float t = wave_sum((float)ha + (float)hc);
+            const float t = wave_sum(__half2float(__ushort_as_half((unsigned short)(bits & 0xffffu))) +
+                                     __half2float(__ushort_as_half((unsigned short)(bits >> 16))));
             if (lane == 0) xsum[b] = t;
         }
     };
