@@ -99,10 +99,10 @@ int env_int(const char* name, int dflt) {
 // outweigh the balance).  Returns false when the balanced kernel does not
 // apply.
 // Rows up to which the balanced kernel is used (env EXL3_GEMV_SK_ROWS, up to
-// 4).  Against the k-split kernel on config 2: m = 2: 13.4 -> 11.9 us;
-// m = 3: 14.5 -> 14.7 us; m = 4: 15.2 -> 16.4 us (each row adds its input
-// rotation to every workgroup and an epilogue wave).
-constexpr int kSkMaxRows = 2;
+// 4).  Against the k-split kernel on config 2 (same run): m = 2: 11.5 ->
+// 11.5 us; m = 3: 14.8 -> 14.0 us; m = 4: 15.2 -> 16.4 us (each row adds its
+// input rotation to every workgroup and an epilogue wave).
+constexpr int kSkMaxRows = 3;
 constexpr int kSkInstRows = 4;
 
 bool plan_gemv_sk(int m, int k, int n, int experts, int* ns_out, int* p_out) {

@@ -394,11 +394,11 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
         float a = __low2float(pr), c = __high2float(pr);
         fwht128_pair_fast(a, c, lane);
         const _Float16 ha = f16_rn(a * kHadNorm), hc = f16_rn(c * kHadNorm);
-        const int ia = xs_index(kk, row, kts_wg), ic = xs_index(kk + 1, row, kts_wg);
-        xs[ia] = ha;
-        xs[ia + 1] = ha;
-        xs[ic] = hc;
-        xs[ic + 1] = hc;
+        // values kk, kk + 1 sit at xs_index(kk) and + 2 (8-byte aligned):
+        // (a, a, c, c) in one 64-bit LDS store
+        const uint32_t da = (uint32_t)__builtin_bit_cast(unsigned short, ha) * 0x10001u;
+        const uint32_t dc = (uint32_t)__builtin_bit_cast(unsigned short, hc) * 0x10001u;
+        *reinterpret_cast<uint2*>(xs + xs_index(kk, row, kts_wg)) = make_uint2(da, dc);
         if constexpr (CB == 2) {
             const float t = wave_sum((float)ha + (float)hc);
             if (lane == 0) xsum[b] = t;

@@ -65,7 +65,7 @@ def test_batched_rejects_bad_arguments():
 
 
 SK_STEPS = (1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16)
-SK_MAX_ROWS = 2  # rows served by the balanced kernel (kSkMaxRows in csrc/exl3_gemv.hip)
+SK_MAX_ROWS = 3  # rows served by the balanced kernel (kSkMaxRows in csrc/exl3_gemv.hip)
 
 
 def _check_plan(m, k, n, K, experts=1):
