@@ -36,6 +36,11 @@ inline int launch_status(const char* what) {
 // so no call's scratch ever overlaps the zeroed regions.
 constexpr size_t kWsCounterBytes = 256 * 1024;
 constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int);
+
+// exl3_gemm: GEMV kernels up to this many rows, the MFMA GEMM above
+// (gemm_gemv_rows(), env override).
+constexpr int kGemmGemvRows = 15;
+int gemm_gemv_rows();
 constexpr size_t kWsAccOffset = kWsCounterBytes;
 constexpr size_t kWsAccBytes = 4 * 1024 * 1024;
 constexpr size_t kWsScratchOffset = kWsAccOffset + kWsAccBytes;

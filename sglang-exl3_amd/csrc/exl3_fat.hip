@@ -43,20 +43,6 @@ __global__ void f32_to_f16_kernel(const float* src, __half* dst, size_t n2) {
     }
 }
 
-// Input rotation of the prefill path: xr = fp16( H(x (.) suh) / sqrt(128) ), one wave per 128 chunk.
-__global__ __launch_bounds__(256) void rotate_rows_kernel(const __half* x, const __half* suh, __half* xr,
-                                                          long long chunks, int k) {
-    const long long chunk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (chunk >= chunks) return;
-    const int lane = threadIdx.x & 63, per_row = k >> 7;
-    const long long row = chunk / per_row;
-    const int c = (int)(chunk - row * per_row) * 128 + 2 * lane;
-    const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)row * k + c), ld_h2(gptr(suh) + c));
-    float a = __low2float(pr), b = __high2float(pr);
-    fwht128_pair_fast(a, b, lane);
-    st_h2(gptr(xr) + (size_t)row * k + c, h2_rn(a * kHadNorm, b * kHadNorm));
-}
-
 struct FatPlan {
     int mt, splits;
 };
@@ -68,15 +54,20 @@ struct FatPlan {
 // under 96 workgroups (an even number of steps per split): its outputs are
 // large, and split outputs cost a zero fill plus one fp32 atomic per value
 // and split, which measured slower than leaving up to 60 % of the CUs idle.
-constexpr int kFatWideRows = 65;
+// Config 2 (n = 14336), narrow against wide: M = 65: 55.9 / 82.8 us, 96: 68.4
+// / 89.6, 128: 109.1 / 98.3, 256: 110.9 / 125.9, 384: 199.5 / 128.2.
+constexpr int kFatWideRows = 112;
+
+bool fat_wide_allowed() {
+    const char* env = getenv("EXL3_FAT_WIDE");
+    return !(env && env[0] == '0');
+}
 
 FatPlan plan_fat(int M, int k, int n) {
     FatPlan pl;
     const int ksteps = k / 64;
     pl.splits = 1;
-    const char* env = getenv("EXL3_FAT_WIDE");
-    const bool wide_on = !(env && env[0] == '0');
-    if (wide_on && M >= kFatWideRows && n % FB_COLS == 0) {
+    if (fat_wide_allowed() && M >= kFatWideRows && n % FB_COLS == 0) {
         pl.mt = FAT_MT_WIDE;
         const long long base = (long long)(n / FB_COLS) * ((M + FB_ROWS - 1) / FB_ROWS);
         while (base * pl.splits < 96 && pl.splits < 16 && ksteps % (4 * pl.splits) == 0) pl.splits *= 2;
@@ -143,7 +134,7 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 
 }  // namespace
 
-// Prefill path of exl3_gemm (m > 64).  Scratch after the workspace's zeroed
+// Prefill path of exl3_gemm (m > gemm_gemv_rows()).  Scratch after the workspace's zeroed
 // regions (shared with the GEMV kernels, which need them to stay zero):
 // [counters][accumulators][xr fp16 m*k][out fp32 m*n, only when the plan
 // splits k; an unsplit GEMM stores fp16 straight to y].
@@ -184,7 +175,7 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
 
 // Gate/up SwiGLU on the MFMA kernels: the input is rotated once with the
 // shared suh into the scratch, then
-//   * up to 64 rows: the narrow kernel in gate/up mode (16- or 64-row tiles,
+//   * below kFatWideRows rows: the narrow kernel in gate/up mode (16- or 64-row tiles,
 //     k-splits toward ~4 workgroups per CU; partial tiles and one counter per
 //     (column block, row tile) in the scratch);
 //   * above: the wide-tile kernel in gate/up mode (one split).
@@ -194,7 +185,7 @@ struct GateUpFatPlan {
 };
 
 GateUpFatPlan plan_gate_up_fat(int m, int k, int n) {
-    if (m > 64) return GateUpFatPlan{FAT_MT_WIDE, 1};
+    if (m >= kFatWideRows && fat_wide_allowed()) return GateUpFatPlan{FAT_MT_WIDE, 1};
     GateUpFatPlan pl{m <= 16 ? 16 : 64, 1};
     const int ksteps = k / 64;
     const long long base = 2LL * (n / 128) * ((m + pl.mt - 1) / pl.mt);
@@ -275,6 +266,6 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, const int16_t* trellis, 
 
 extern "C" size_t exl3_gemm_workspace_size(int m, int k, int n, int K) {
     if (m < 1 || k < 128 || n < 128) return 0;
-    if (m <= 64) return exl3_gemv_workspace_size(m, k, n, K, 1);
+    if (m <= gemm_gemv_rows()) return exl3_gemv_workspace_size(m, k, n, K, 1);
     return fat_gemm_scratch_bytes(m, k, n);
 }

@@ -59,6 +59,17 @@ int gemv_launch(int K, int cb, int mb, const GemvParams& p, int experts, hipStre
 int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,
                   int m, int k, int n, int K, int cb, void* ws, size_t ws_bytes, hipStream_t st);
 
+// Rows up to which exl3_gemm runs the GEMV kernels; above, the input is
+// rotated once and the MFMA GEMM runs (env EXL3_GEMM_GEMV_ROWS, at most 64).
+// Graph-timed on config 2 (k=4096, n=14336, K=4), GEMV kernels against the
+// MFMA path: m = 8: 19.3 / 25.9 us, 12: 22.9 / 26.3, 16: 30.7 / 29.3,
+// 32: 58.1 / 33.9, 64: 116.9 / 53.0.
+int gemm_gemv_rows() {
+    const char* v = getenv("EXL3_GEMM_GEMV_ROWS");
+    const int r = (v && *v) ? atoi(v) : kGemmGemvRows;
+    return r < 0 ? 0 : (r > 64 ? 64 : r);
+}
+
 namespace {
 
 constexpr int kMaxGemvRows = 64;
@@ -169,11 +180,32 @@ GemvPlan plan_gemv(int m, int k, int n, int K, int experts) {
     return best;
 }
 
-size_t workspace_bytes_for(const GemvPlan& pl, int m, int n, int experts) {
-    if (pl.sk) return kWsAccOffset + (size_t)m * n * 8;
+// Rows from which a single-matrix k-split GEMV rotates its input once, in a
+// launch of its own, instead of in every workgroup (each workgroup rotates
+// every row of its k range).  Config 2, per-workgroup against separate
+// rotation: m = 4: 15.4 / 16.4 us, 8: 19.0 / 19.8, 16: 30.6 / 30.3, 32: 62.2 /
+// 57.8, 64: 126.9 / 116.2 (the launch costs ~1 us).  Env EXL3_GEMV_ROT_ROWS
+// overrides (0: never).
+constexpr int kGemvRotRows = 32;
+
+bool gemv_pre_rotates(const GemvPlan& pl, int m, int experts) {
+    const int rows = env_int("EXL3_GEMV_ROT_ROWS", kGemvRotRows);
+    return !pl.sk && experts == 1 && rows > 0 && m >= rows;
+}
+
+// Workspace: [counters][accumulators][partials (k-split), then the rotated
+// rows (pre-rotating calls)].
+size_t gemv_partials_bytes(const GemvPlan& pl, int m, int n, int experts) {
     if (pl.splits <= 1) return 0;
-    const size_t nblk = (size_t)(n / 128) * experts;
-    return kWsScratchOffset + nblk * pl.splits * (size_t)m * 128 * sizeof(float);
+    return (((size_t)(n / 128) * experts * pl.splits * (size_t)m * 128 * sizeof(float)) + 255) & ~(size_t)255;
+}
+
+size_t workspace_bytes_for(const GemvPlan& pl, int m, int k, int n, int experts) {
+    if (pl.sk) return kWsAccOffset + (size_t)m * n * 8;
+    const size_t part = gemv_partials_bytes(pl, m, n, experts);
+    const size_t xr = gemv_pre_rotates(pl, m, experts) ? (size_t)m * k * 2 : 0;
+    if (part == 0 && xr == 0) return 0;
+    return kWsScratchOffset + part + xr;
 }
 
 int check_common(const char* fn, int m, int k, int n, int K, int codebook) {
@@ -188,7 +220,7 @@ int check_common(const char* fn, int m, int k, int n, int K, int codebook) {
 int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, void* ws, size_t ws_bytes,
              hipStream_t st) {
     GemvPlan pl = plan_gemv(p.m, p.k, p.n, K, experts);
-    const size_t need = workspace_bytes_for(pl, p.m, p.n, experts);
+    const size_t need = workspace_bytes_for(pl, p.m, p.k, p.n, experts);
     EXL3_REQUIRE_CODE(need == 0 || (ws && ws_bytes >= need), EXL3_ERR_WORKSPACE,
                       "%s: workspace of %zu bytes needed, %zu given", fn, need, ws ? ws_bytes : (size_t)0);
     if (pl.sk) {
@@ -217,6 +249,16 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
     } else {
         p.counters = nullptr;
         p.partials = nullptr;
+    }
+    if (gemv_pre_rotates(pl, p.m, experts) && !p.gu) {
+        __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsScratchOffset +
+                                               gemv_partials_bytes(pl, p.m, p.n, experts));
+        const long long chunks = (long long)p.m * (p.k / 128);
+        rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(p.x, p.suh, xr, chunks, p.k);
+        const int rc = launch_status("exl3 gemv rotate launch");
+        if (rc) return rc;
+        p.x = xr;
+        p.x_rot = 1;
     }
     return gemv_launch(K, codebook, pl.mb, p, experts, st);
 }
@@ -329,7 +371,7 @@ extern "C" size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int exper
     if (m < 1 || k < 128 || n < 128 || experts < 1) return 0;
     const int mc = m > kMaxGemvRows ? kMaxGemvRows : m;
     GemvPlan pl = plan_gemv(mc, k, n, K, experts);
-    return workspace_bytes_for(pl, mc, n, experts);
+    return workspace_bytes_for(pl, mc, k, n, experts);
 }
 
 extern "C" int exl3_gemv_plan(int m, int k, int n, int K, int experts, int* out) {
@@ -371,7 +413,7 @@ extern "C" int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16
     EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4) && aligned(svh, 4) && aligned(trellis, 16),
                  "exl3_gemm: misaligned pointer");
     hipStream_t st = as_stream(stream);
-    if (m > kMaxGemvRows) return fat_gemm_rows(x, trellis, suh, svh, y, m, k, n, K, codebook, workspace,
+    if (m > gemm_gemv_rows()) return fat_gemm_rows(x, trellis, suh, svh, y, m, k, n, K, codebook, workspace,
                                                workspace_bytes, st);
     for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
         const int mc = (m - r0) < kMaxGemvRows ? (m - r0) : kMaxGemvRows;

@@ -58,6 +58,9 @@ struct GemvParams {
     const __half* suh2;
     const __half* svh2;
     float limit;
+    // x holds the rows already rotated (x (.) suh, FWHT, / sqrt(128), fp16;
+    // rotate_rows_kernel): the workgroups stage them as they are
+    int x_rot;
 };
 
 // Steps of weight words a wave keeps in flight.  Measured on MI355X (config 2,
@@ -318,7 +321,7 @@ __device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[D][K], const EXL
 
 // GU: the gate/up SwiGLU mode (p.gu), a separate instance so that the plain
 // GEMV carries none of its registers (71 against 199 VGPRs at K=4).
-template <int K, int CB, int MB, int NS, bool GU>
+template <int K, int CB, int MB, int NS, bool GU, bool XR = false>
 __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     constexpr int D = gv_depth<K>();
     extern __shared__ __align__(16) unsigned char gv_smem[];
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
             const int row = b / nblk128, bb = b - row * nblk128;
             const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
             xpre[j] = ld_h2(x + (size_t)row * k + kg);
-            spre[j] = ld_h2(suhg + kg);
+            if constexpr (!XR) spre[j] = ld_h2(suhg + kg);
         }
     }
     // output scale of this lane's two columns, requested now: the epilogue
@@ -390,17 +393,26 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     auto rotate = [&](int b, __half2 xv, __half2 sv) {
         const int row = b / nblk128, bb = b - row * nblk128;
         const int kk = bb * 128 + 2 * lane;
-        const __half2 pr = __hmul2(xv, sv);
-        float a = __low2float(pr), c = __high2float(pr);
-        fwht128_pair_fast(a, c, lane);
-        const _Float16 ha = f16_rn(a * kHadNorm), hc = f16_rn(c * kHadNorm);
+        uint32_t bits;
+        if constexpr (XR) {
+            (void)sv;
+            bits = *reinterpret_cast<const uint32_t*>(&xv);
+        } else {
+            const __half2 pr = __hmul2(xv, sv);
+            float a = __low2float(pr), c = __high2float(pr);
+            fwht128_pair_fast(a, c, lane);
+            const _Float16 ha = f16_rn(a * kHadNorm), hc = f16_rn(c * kHadNorm);
+            bits = (uint32_t)__builtin_bit_cast(unsigned short, ha) |
+                   ((uint32_t)__builtin_bit_cast(unsigned short, hc) << 16);
+        }
         // values kk, kk + 1 sit at xs_index(kk) and + 2 (8-byte aligned):
         // (a, a, c, c) in one 64-bit LDS store
-        const uint32_t da = (uint32_t)__builtin_bit_cast(unsigned short, ha) * 0x10001u;
-        const uint32_t dc = (uint32_t)__builtin_bit_cast(unsigned short, hc) * 0x10001u;
+        const uint32_t da = __builtin_amdgcn_perm(bits, bits, 0x01000100u);
+        const uint32_t dc = __builtin_amdgcn_perm(bits, bits, 0x03020302u);
         *reinterpret_cast<uint2*>(xs + xs_index(kk, row, kts_wg)) = make_uint2(da, dc);
         if constexpr (CB == 2) {
-            const float t = wave_sum((float)ha + (float)hc);
+            const float t = wave_sum(__half2float(__ushort_as_half((unsigned short)(bits & 0xffffu))) +
+                                     __half2float(__ushort_as_half((unsigned short)(bits >> 16))));
             if (lane == 0) xsum[b] = t;
         }
     };
@@ -412,7 +424,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     for (int b = wave + GV_PRE * nwaves; b < nrot; b += nwaves) {
         const int row = b / nblk128, bb = b - row * nblk128;
         const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
-        rotate(b, ld_h2(x + (size_t)row * k + kg), ld_h2(suhg + kg));
+        rotate(b, ld_h2(x + (size_t)row * k + kg), XR ? __half2{} : ld_h2(suhg + kg));
     }
     __syncthreads();
 
@@ -530,6 +542,24 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     }
 }
 
+namespace {
+// Input rotation of a row batch: xr = fp16( H(x (.) suh) / sqrt(128) ), one
+// wave per 128-wide chunk (feeds the k-split GEMV's pre-rotated mode and the
+// MFMA GEMM).
+__global__ __launch_bounds__(256) void rotate_rows_kernel(const __half* x, const __half* suh, __half* xr,
+                                                          long long chunks, int k) {
+    const long long chunk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (chunk >= chunks) return;
+    const int lane = threadIdx.x & 63, per_row = k >> 7;
+    const long long row = chunk / per_row;
+    const int c = (int)(chunk - row * per_row) * 128 + 2 * lane;
+    const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)row * k + c), ld_h2(gptr(suh) + c));
+    float a = __low2float(pr), b = __high2float(pr);
+    fwht128_pair_fast(a, b, lane);
+    st_h2(gptr(xr) + (size_t)row * k + c, h2_rn(a * kHadNorm, b * kHadNorm));
+}
+}  // namespace
+
 // Dynamic LDS bytes of gemv_kernel for (m, k-slices per workgroup, kw).
 inline size_t gemv_smem_bytes(int m, int kts_wg, int kw) {
     const size_t xs = ((size_t)kts_wg * 4 * m * 8 * 2 + 16 + 15) & ~(size_t)15;
@@ -541,16 +571,19 @@ int gemv_launch_k(int cb, int mb, const GemvParams& p, int experts, hipStream_t 
     dim3 grid(p.n / 128, p.splits, experts);
     const size_t smem = gemv_smem_bytes(p.m, 4 * p.nsteps * p.kw, p.kw);
     const int threads = 256 * p.kw;
-#define EXL3_GV_GU(CBV, MBV, NSV, GUV)                                                                 \
-    if (cb == CBV && mb == MBV && p.nsteps == NSV && (p.gu != 0) == GUV) {                             \
-        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV, GUV>);           \
+#define EXL3_GV_GU(CBV, MBV, NSV, GUV, XRV)                                                            \
+    if (cb == CBV && mb == MBV && p.nsteps == NSV && (p.gu != 0) == GUV && (p.x_rot != 0) == XRV) {    \
+        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV, GUV, XRV>);      \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 gemv");                                      \
         if (lrc) return lrc;                                                                           \
-        gemv_kernel<K, CBV, MBV, NSV, GUV><<<grid, threads, smem, st>>>(p);                            \
+        gemv_kernel<K, CBV, MBV, NSV, GUV, XRV><<<grid, threads, smem, st>>>(p);                       \
         return launch_status("exl3 gemv launch");                                                      \
     }
-// gate/up mode runs with one row block (m <= 4)
-#define EXL3_GV_NS(CBV, MBV, NSV) EXL3_GV_GU(CBV, MBV, NSV, false) if constexpr (MBV == 1) EXL3_GV_GU(CBV, MBV, NSV, true)
+// gate/up mode runs with one row block (m <= 4); pre-rotated rows only in the
+// plain mode
+#define EXL3_GV_NS(CBV, MBV, NSV)                                                                      \
+    EXL3_GV_GU(CBV, MBV, NSV, false, false) EXL3_GV_GU(CBV, MBV, NSV, false, true)                     \
+    if constexpr (MBV == 1) EXL3_GV_GU(CBV, MBV, NSV, true, false)
 #define EXL3_GV_CASE(CBV, MBV) \
     EXL3_GV_NS(CBV, MBV, 2) EXL3_GV_NS(CBV, MBV, 4) EXL3_GV_NS(CBV, MBV, 8) EXL3_GV_NS(CBV, MBV, 16)
     EXL3_GV_CASE(0, 1) EXL3_GV_CASE(0, 2) EXL3_GV_CASE(0, 4)

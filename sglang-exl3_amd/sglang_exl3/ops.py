@@ -125,9 +125,10 @@ def dequant_trellis_impl(trellis, suh, svh, bits, mcg):
     return W
 
 
-def _gemv_like(name, fn, x, trellis, suh, svh, K, cb, max_rows=None):
-    """y (fp16 [rows, n]) = x (fp16 [..., k]) @ W through `fn` (exl3_gemv or
-    exl3_gemm); every shape the kernels trust is checked here first."""
+def _gemv_like(name, fn, x, trellis, suh, svh, K, cb, max_rows=None, gemv=False):
+    """y (fp16 [rows, n]) = x (fp16 [..., k]) @ W through `fn` (exl3_gemv when
+    `gemv`, else exl3_gemm), with the workspace that entry point asks for;
+    every shape the kernels trust is checked here first."""
     _require_device(name, x, trellis, suh, svh)
     _check_trellis(name, trellis, K)
     if x.dim() < 2:
@@ -153,7 +154,8 @@ def _gemv_like(name, fn, x, trellis, suh, svh, K, cb, max_rows=None):
         return y
     lib = _lib.lib()
     with torch.cuda.device(x.device):
-        need = int(lib.exl3_gemm_workspace_size(m, kdim, n, int(K)))
+        need = int(lib.exl3_gemv_workspace_size(m, kdim, n, int(K), 1) if gemv
+                   else lib.exl3_gemm_workspace_size(m, kdim, n, int(K)))
         ws = workspace(x.device, need) if need else None
         rc = fn(x2.data_ptr(), tr.data_ptr(), suh.data_ptr(), svh.data_ptr(), y.data_ptr(), m, kdim, n,
                 int(K), int(cb), 0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
@@ -166,7 +168,7 @@ def exl3_gemv_impl(x, trellis, suh, svh, K, mcg, mmode=1):
     if mmode not in (0, 1):
         raise RuntimeError("sglang_exl3::exl3_gemv: mmode must be 0 or 1")
     return _gemv_like("exl3_gemv", _lib.lib().exl3_gemv, x, trellis, suh, svh, K,
-                      _lib.codebook_from_mcg(bool(mcg)), max_rows=64)
+                      _lib.codebook_from_mcg(bool(mcg)), max_rows=64, gemv=True)
 
 
 def exl3_gemm_impl(x, trellis, suh, svh, K, mcg):
