@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "../../include/sglang_exl3_amd.h"
 
@@ -37,10 +38,6 @@ inline int launch_status(const char* what) {
 constexpr size_t kWsCounterBytes = 256 * 1024;
 constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int);
 
-// exl3_gemm: GEMV kernels up to this many rows, the MFMA GEMM above
-// (gemm_gemv_rows(), env override).
-constexpr int kGemmGemvRows = 15;
-int gemm_gemv_rows();
 constexpr size_t kWsAccOffset = kWsCounterBytes;
 constexpr size_t kWsAccBytes = 4 * 1024 * 1024;
 constexpr size_t kWsScratchOffset = kWsAccOffset + kWsAccBytes;
@@ -54,6 +51,19 @@ constexpr size_t kMaxLds = 160 * 1024;
 int allow_dynamic_lds(const void* kernel, size_t need, const char* what);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Integer value of environment variable `name` (tuning overrides, read per
+// call), or `dflt` when it is unset or empty.
+inline int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+// exl3_gemm: GEMV kernels up to this many rows, the MFMA GEMM above
+// (gemm_gemv_rows(), env override).
+constexpr int kGemmGemvRows = 15;
+int gemm_gemv_rows();
 
 }  // namespace exl3
 

@@ -47,16 +47,20 @@ struct FatPlan {
     int mt, splits;
 };
 
-// Wide tiles (256 x 256, fat_big_kernel) from kFatWideRows rows on (env
-// EXL3_FAT_WIDE=0 turns them off); below, rows per tile from M.  k-splits for
-// the narrow kernel toward ~4 workgroups per CU (each split a whole number of
-// FAT_CH chunks), capped by the atomics they add.  The wide kernel splits only grids
-// under 96 workgroups (an even number of steps per split): its outputs are
-// large, and split outputs cost a zero fill plus one fp32 atomic per value
-// and split, which measured slower than leaving up to 60 % of the CUs idle.
-// Config 2 (n = 14336), narrow against wide: M = 65: 55.9 / 82.8 us, 96: 68.4
-// / 89.6, 128: 109.1 / 98.3, 256: 110.9 / 125.9, 384: 199.5 / 128.2.
-constexpr int kFatWideRows = 112;
+// Wide tiles (256 x 256, fat_big_kernel) above kFatNarrowMaxRows rows (env
+// EXL3_FAT_WIDE=0 turns them off); up to there the narrow kernel with 16-row
+// tiles up to 16 rows and 64-row tiles above.  k-splits for the narrow kernel
+// toward ~4 workgroups per CU (each split a whole number of FAT_CH chunks),
+// capped by the atomics they add.  The wide kernel splits only grids under 96
+// workgroups (an even number of steps per split): its outputs are large, and
+// split outputs cost a zero fill plus one fp32 atomic per value and split,
+// which measured slower than leaving up to 60 % of the CUs idle.
+// Config 2 (n = 14336), graph-timed: 64-row narrow tiles / 128-row narrow
+// tiles / wide tiles: M = 128: 68.7 / 108.8 / 99.0 us, 192: 78.0 / 109.6 /
+// 111.7, 256: 81.0 / 110.7 / 125.3, 320: 128.8 / 172.0 / 126.8, 512: 154.8 /
+// 222.6 / 129.6, 768: 227.9 / 330.7 / 131.4.  128-row narrow tiles never win
+// (kept as the EXL3_FAT_MT=128 override).
+constexpr int kFatNarrowMaxRows = 256;
 
 bool fat_wide_allowed() {
     const char* env = getenv("EXL3_FAT_WIDE");
@@ -67,13 +71,15 @@ FatPlan plan_fat(int M, int k, int n) {
     FatPlan pl;
     const int ksteps = k / 64;
     pl.splits = 1;
-    if (fat_wide_allowed() && M >= kFatWideRows && n % FB_COLS == 0) {
+    if (fat_wide_allowed() && M > kFatNarrowMaxRows && n % FB_COLS == 0) {
         pl.mt = FAT_MT_WIDE;
         const long long base = (long long)(n / FB_COLS) * ((M + FB_ROWS - 1) / FB_ROWS);
         while (base * pl.splits < 96 && pl.splits < 16 && ksteps % (4 * pl.splits) == 0) pl.splits *= 2;
         return pl;
     }
-    pl.mt = M >= 128 ? 128 : (M > 16 ? 64 : 16);
+    pl.mt = M > 16 ? 64 : 16;
+    const int fmt = env_int("EXL3_FAT_MT", 0);  // tuning override: 16, 64 or 128 rows per tile
+    if (fmt == 16 || fmt == 64 || fmt == 128) pl.mt = fmt;
     const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
     const char* fs = getenv("EXL3_FAT_SPLITS");  // tuning override (power of two)
     const int forced = fs ? atoi(fs) : 0;
@@ -175,17 +181,21 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
 
 // Gate/up SwiGLU on the MFMA kernels: the input is rotated once with the
 // shared suh into the scratch, then
-//   * below kFatWideRows rows: the narrow kernel in gate/up mode (16- or 64-row tiles,
-//     k-splits toward ~4 workgroups per CU; partial tiles and one counter per
-//     (column block, row tile) in the scratch);
+//   * up to kGateUpNarrowMaxRows rows: the narrow kernel in gate/up mode (16- or
+//     64-row tiles, k-splits toward ~4 workgroups per CU; partial tiles and one
+//     counter per (column block, row tile) in the scratch);
 //   * above: the wide-tile kernel in gate/up mode (one split).
+// Config 3 (n = 14336 per projection), narrow / wide: M = 112: 109.4 / 129.1 us,
+// 128: 122.9 / 129.3, 144: 155.0 / 129.4, 256: 227.9 / 133.3.
+constexpr int kGateUpNarrowMaxRows = 128;
+
 // Scratch: [counters][accumulators][xr fp16 m*k][partials, narrow only].
 struct GateUpFatPlan {
     int mt, splits;
 };
 
 GateUpFatPlan plan_gate_up_fat(int m, int k, int n) {
-    if (m >= kFatWideRows && fat_wide_allowed()) return GateUpFatPlan{FAT_MT_WIDE, 1};
+    if (m > kGateUpNarrowMaxRows && fat_wide_allowed()) return GateUpFatPlan{FAT_MT_WIDE, 1};
     GateUpFatPlan pl{m <= 16 ? 16 : 64, 1};
     const int ksteps = k / 64;
     const long long base = 2LL * (n / 128) * ((m + pl.mt - 1) / pl.mt);

@@ -83,12 +83,6 @@ struct GemvPlan {
     int sk;      // 1: balanced kernel (gemv_sk_kernel, m <= 4): splits = pieces per column block, nsteps = piece length
 };
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    if (!v || !*v) return dflt;
-    return atoi(v);
-}
-
 // gfx950 launch shape.  Every workgroup covers one 128-column block (one
 // output FWHT block) with 4 column waves, times kw k-waves, each walking
 // `nsteps` steps of 4 k-slices.  Walk from the most work per wave to the least

@@ -343,12 +343,6 @@ struct MoePlan {
     int ns, kw, splits, bpi;
 };
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    if (!v || !*v) return dflt;
-    return atoi(v);
-}
-
 // Active experts expected for `tokens` tokens routed to `topk` of E experts
 // uniformly: E (1 - (1 - topk/E)^tokens), capped by the slot count.
 double expected_active(int tokens, int topk, int E) {

@@ -1,5 +1,5 @@
 """GPU parity of the many-row MFMA GEMM: exl3_fat_gemm / exl3_fat_gemm_scatter
-(rotated fp16 input, fp32 output) and exl3_gemm's prefill path (m > 64),
+(rotated fp16 input, fp32 output) and exl3_gemm's prefill path (m ≥ 16),
 against the oracle (bar: max-abs-err <= 2e-2 * rms(ref), cosine >= 0.9999)."""
 
 import numpy as np
@@ -80,7 +80,7 @@ def _fat(a, tr, sv, K, cb, M, n):
 @pytest.mark.parametrize("K", range(1, 9))
 @pytest.mark.parametrize("cb", [0, 1, 2])
 def test_fat_wide_tiles_every_width(K, cb):
-    """Wide-tile kernel (256 x 256 tiles, from 65 rows): every bit width and codebook,
+    """Wide-tile kernel (256 x 256 tiles, above 256 rows): every bit width and codebook,
     a partial second row tile (ending in the first row half), k-splits accumulating atomically."""
     M, k, n = 300, 256, 256
     print(f"case: fat wide M={M} k={k} n={n} K={K} cb={cb}", flush=True)
@@ -102,7 +102,7 @@ def test_fat_wide_and_narrow_kernels(M, k, n, K, cb, wide):
 
 
 def test_fat_wide_scatter_accumulates():
-    M, k, n, K = 150, 512, 512, 3
+    M, k, n, K = 300, 512, 512, 3
     tr, su, sv = make_weight(k, n, K, seed=15)
     a = _rotate(make_x(M, k, seed=16), su)
     rng = np.random.default_rng(17)
