@@ -266,8 +266,9 @@ __device__ __forceinline__ uint32_t window_mid(const uint32_t* buf, const uint32
 
 // ---------------------------------------------------------------- codebooks
 
-// x = state * M (+ 64248484 for 3INST) mod 2^32.  v_mul_lo_u32 issues at the
-// full VALU rate on gfx950 (measured: same throughput as v_fma_f32).
+// x = state * M (+ 64248484 for 3INST) mod 2^32: one v_mul_lo_u32 (a
+// 4-cycle VALU op on gfx950, like v_bfe_u32; building the product from
+// 16-bit pieces takes at least two such ops).
 template <int CB>
 __device__ __forceinline__ uint32_t hash(uint32_t s) {
     constexpr uint32_t M = CB == 0 ? 89226354u : CB == 1 ? 0xCBAC1FEDu : 0x83DCD12Du;
