@@ -67,6 +67,42 @@ bool fat_wide_allowed() {
     return !(env && env[0] == '0');
 }
 
+// Compute units of the current device (one wide-tile workgroup each), cached
+// per device.
+int fat_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] <= 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+// Tiles of a one-split wide-tile launch that run as two k-halves (the tail
+// split): the tiles of a last round that would fill at most half the CUs
+// (or all tiles, when there are at most half as many as CUs).  Graph-timed,
+// split vs whole (k = 4096, K = 3): gate/up n = 14336, M = 160 / 256 / 2048 /
+// 2560: 96.7 / 99.9 / 546.9 / 678.0 vs 130.4 / 133.1 / 551.9 / 696.6 us;
+// exl3_gemm n = 14336, M = 300 / 512: 91.8 / 95.4 vs 126.7 / 130.0, n = 28672,
+// M = 768 / 2048: 221.7 / 522.2 vs 257.8 / 534.1.  Env EXL3_FAT_TAIL=0 turns
+// it off.
+int fat_tail_tiles(int tiles, int ksteps) {
+    if (ksteps % 4 != 0 || env_int("EXL3_FAT_TAIL", 1) == 0) return 0;
+    const int c = fat_cus(), r = tiles % c;
+    return (r > 0 && 2 * r <= c) ? r : 0;
+}
+size_t fat_tail_bytes(int tail) { return (size_t)tail * FB_TAIL_FLOATS * sizeof(float); }
+
+// Tail tiles of the wide kernel for an unsplit (m, k, n) call (gate/up mode:
+// n per projection, one tile per 128-column block of each).
+int wide_tail_tiles(int m, int k, int n, bool gu) {
+    const int tiles = (gu ? n / 128 : n / FB_COLS) * ((m + FB_ROWS - 1) / FB_ROWS);
+    return fat_tail_tiles(tiles, k / 64);
+}
+
 FatPlan plan_fat(int M, int k, int n) {
     FatPlan pl;
     const int ksteps = k / 64;
@@ -106,11 +142,20 @@ int check_fat(const char* fn, const void* a, const void* trellis, const void* ou
     return EXL3_OK;
 }
 
+// tail: tail-split tiles (unsplit wide launch with fp16 output; 0 = none),
+// their hand-off tiles at tail_part and counts / flags at tail_sync.
 int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out16, const uint16_t* svh,
             const int64_t* token_idx, const uint16_t* route_w, int M, int k, int n, int K, int cb, bool zero_first,
-            hipStream_t st) {
+            hipStream_t st, int tail = 0, char* tail_part = nullptr, int* tail_sync = nullptr) {
     const FatPlan pl = plan_fat(M, k, n);
     FatParams p{};
+    if (tail > 0) {
+        p.tiles_x = n / FB_COLS;
+        p.tail_tiles = tail;
+        p.tail_first = p.tiles_x * ((M + FB_ROWS - 1) / FB_ROWS) - tail;
+        p.tail_part = reinterpret_cast<float*>(tail_part);
+        p.tail_sync = tail_sync;
+    }
     p.a = reinterpret_cast<const __half*>(a);
     p.trellis = reinterpret_cast<const uint32_t*>(trellis);
     p.svh = reinterpret_cast<const __half*>(svh);
@@ -141,13 +186,16 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 }  // namespace
 
 // Prefill path of exl3_gemm (m > gemm_gemv_rows()).  Scratch after the workspace's zeroed
-// regions (shared with the GEMV kernels, which need them to stay zero):
-// [counters][accumulators][xr fp16 m*k][out fp32 m*n, only when the plan
-// splits k; an unsplit GEMM stores fp16 straight to y].
+// regions (shared with the GEMV kernels, which need them to stay zero); an
+// unsplit GEMM stores fp16 straight to y.
 size_t fat_xr_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
+// [counters][accumulators][xr fp16 m*k][out fp32 m*n, only when the plan
+// splits k | tail-split hand-off tiles, only for an unsplit wide launch].
 size_t fat_gemm_scratch_bytes(int m, int k, int n) {
-    const bool split = plan_fat(m, k, n).splits > 1;
-    return kWsScratchOffset + fat_xr_bytes(m, k) + (split ? (size_t)m * n * 4 : 0);
+    const FatPlan pl = plan_fat(m, k, n);
+    const bool split = pl.splits > 1;
+    const size_t tail = (!split && pl.mt == FAT_MT_WIDE) ? fat_tail_bytes(wide_tail_tiles(m, k, n, false)) : 0;
+    return kWsScratchOffset + fat_xr_bytes(m, k) + (split ? (size_t)m * n * 4 : tail);
 }
 
 int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,
@@ -167,8 +215,10 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
     if (rc) return rc;
     const FatPlan pl = plan_fat(m, k, n);
     if (pl.splits == 1) {
+        const int tail = pl.mt == FAT_MT_WIDE ? wide_tail_tiles(m, k, n, false) : 0;
         return run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, nullptr, reinterpret_cast<__half*>(y), svh,
-                       nullptr, nullptr, m, k, n, K, cb, false, st);
+                       nullptr, nullptr, m, k, n, K, cb, false, st, tail, reinterpret_cast<char*>(o32),
+                       reinterpret_cast<int*>(ws));
     }
     rc = run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, o32, nullptr, svh, nullptr, nullptr, m, k, n, K, cb,
                  true, st);
@@ -209,6 +259,7 @@ size_t fat_gate_up_scratch_bytes(int m, int k, int n) {
     const GateUpFatPlan pl = plan_gate_up_fat(m, k, n);
     size_t b = kWsScratchOffset + fat_xr_bytes(m, k);
     if (pl.mt != FAT_MT_WIDE) b += (size_t)2 * (n / 128) * pl.splits * (size_t)m * 128 * sizeof(float);
+    else b += fat_tail_bytes(wide_tail_tiles(m, k, n, true));
     return b;
 }
 
@@ -248,6 +299,16 @@ int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate
     p.limit = limit;
     p.counters = reinterpret_cast<int*>(w8);
     p.partials = reinterpret_cast<float*>(w8 + kWsScratchOffset + fat_xr_bytes(m, k));
+    if (pl.mt == FAT_MT_WIDE) {
+        const int tail = wide_tail_tiles(m, k, n, true);
+        if (tail > 0) {
+            p.tiles_x = n / 128;
+            p.tail_tiles = tail;
+            p.tail_first = p.tiles_x * ((m + FB_ROWS - 1) / FB_ROWS) - tail;
+            p.tail_part = p.partials;
+            p.tail_sync = p.counters;
+        }
+    }
     return fat_launch(K, cb, pl.mt, p, pl.splits, st);
 }
 

@@ -85,6 +85,16 @@ struct FatParams {
     const int64_t* tabs[9];
     float* g32;
     const int* rows_map;
+    // Tail split of the wide-tile kernel (one k-split, plain stores; 1-D grid
+    // when tail_tiles > 0): tiles [0, tail_first) run whole, each of the
+    // tail_tiles tiles after them as two k-halves (workgroups tail_first + 2j
+    // and + 1 for tile tail_first + j), so a last round of workgroups that
+    // would leave at least half the CUs idle fills them.  The first half to
+    // finish stores its accumulators device-coherently in tail_part and
+    // raises a flag; the second adds them to its own and runs the epilogue.
+    int tail_first, tail_tiles, tiles_x;
+    float* tail_part;  // [tail_tiles][FB_TAIL_FLOATS]
+    int* tail_sync;    // [tail_tiles] arrival counts, then [tail_tiles] flags; zero between calls
 };
 
 template <int K>
@@ -354,6 +364,11 @@ constexpr int FB_B_BYTES = 4 * 2 * 4 * 64 * 16;  // one step's B fragments: [qua
 constexpr int FB_PASS_ROWS = 64;                // epilogue rows per LDS pass (32 of each half)
 constexpr int FB_CTS = FB_COLS + 4;             // epilogue row stride (floats)
 constexpr int FAT_MT_WIDE = 0;                  // plan value (rows per tile) selecting fat_big_kernel
+constexpr int FB_TAIL_FLOATS = FB_ROWS * FB_COLS;  // one tile's fp32 accumulators (tail split)
+// Polls (each followed by an s_sleep of ~0.2 us) after which the second half
+// of a split tile stops waiting for the first (~0.25 s, far beyond a tile;
+// a bound so that every wave exits even if the first half never stored).
+constexpr int kFatTailPolls = 1 << 20;
 
 constexpr size_t fat_big_smem_bytes() {
     constexpr size_t stage = 2 * (size_t)FB_A_BYTES + 2 * (size_t)FB_B_BYTES;
@@ -410,15 +425,30 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
     extern __shared__ __align__(16) unsigned char fat_smem[];
     unsigned char* const bsm = fat_smem + 2 * FB_A_BYTES;
 
-    const int bx = blockIdx.x, sidx = blockIdx.z;
-    const int m0 = blockIdx.y * FB_ROWS;
+    // tile of this workgroup (and, tail split, which k-half of it: -1 whole)
+    int bx = blockIdx.x, by = blockIdx.y, half = -1, slot = 0;
+    if (p.tail_tiles > 0) {
+        int lin = blockIdx.x;
+        if (lin >= p.tail_first) {
+            slot = (lin - p.tail_first) >> 1;
+            half = (lin - p.tail_first) & 1;
+            lin = p.tail_first + slot;
+        }
+        // wave-uniform: kept in scalar registers
+        by = __builtin_amdgcn_readfirstlane(lin / p.tiles_x);
+        bx = __builtin_amdgcn_readfirstlane(lin - by * p.tiles_x);
+        half = __builtin_amdgcn_readfirstlane(half);
+        slot = __builtin_amdgcn_readfirstlane(slot);
+    }
+    const int sidx = blockIdx.z;
+    const int m0 = by * FB_ROWS;
     const int rows = min(FB_ROWS, p.M - m0);
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
     const int rh = wv >> 2, cq = wv & 3;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
     const int ntiles = p.n >> 4;
-    const int nsteps = p.ksteps;  // even
-    const int kt0 = sidx * nsteps * 4;
+    const int nsteps = half >= 0 ? p.ksteps / 2 : p.ksteps;  // even
+    const int kt0 = sidx * p.ksteps * 4 + (half > 0 ? nsteps * 4 : 0);
     // this wave decodes group rh of quarter cq: column tiles 4cq + 2rh + (i >> 3)
     // (gate/up mode: quarters 0, 1 of the gate block bx, 2, 3 of the up block bx)
     const int nt = GU ? bx * 8 + (cq & 1) * 4 + rh * 2 + (i >> 3) : bx * (FB_COLS / 16) + cq * 4 + rh * 2 + (i >> 3);
@@ -541,6 +571,53 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
     }
     __syncthreads();  // everything landed before the epilogue reuses the LDS
 
+    if (half >= 0) {
+        // tail split: the first half to get here hands its accumulators to
+        // the second (one device-coherent store and load per value; fp32
+        // addition is commutative, so the sum does not depend on which half
+        // came first)
+        __shared__ int tail_old;
+        if (tid == 0) tail_old = __hip_atomic_fetch_add(p.tail_sync + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        // pair j of thread t at [j][t]: each store covers 512 consecutive bytes
+        unsigned long long* part = reinterpret_cast<unsigned long long*>(p.tail_part + (size_t)slot * FB_TAIL_FLOATS) + tid;
+        int* flag = p.tail_sync + p.tail_tiles + slot;
+        if (tail_old == 0) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int G = 0; G < 2; ++G)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int j = ((rb * 2 + G) * 2 + c) * 2 + h;
+                            const float2 v = make_float2(acc[rb][G][c][2 * h], acc[rb][G][c][2 * h + 1]);
+                            __hip_atomic_store(part + (size_t)j * FB_THREADS, *reinterpret_cast<const unsigned long long*>(&v),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+            wait_stores();
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        if (tid == 0) {
+            for (int it = 0; it < kFatTailPolls; ++it) {
+                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+                __builtin_amdgcn_s_sleep(8);
+            }
+            __hip_atomic_store(p.tail_sync + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        // the first half's sums are added as the epilogue moves the
+        // accumulators to LDS (adding them into the accumulators here would
+        // keep a second copy of all 128 live)
+    }
+    const unsigned long long* tail_other =
+        half >= 0 ? reinterpret_cast<const unsigned long long*>(p.tail_part + (size_t)slot * FB_TAIL_FLOATS) + tid
+                  : nullptr;
+
     // epilogue: 4 passes through LDS, pass p holding tile rows 32p .. +32 of
     // each half (LDS row rh*32 + local); the output FWHT, norm and svh per
     // (row, 128-block).  Accumulator (rb, G, c, r) is tile row
@@ -555,13 +632,26 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
 #pragma unroll
             for (int G = 0; G < 2; ++G)
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
+                for (int c = 0; c < 2; ++c) {
+                    float o[4] = {0.f, 0.f, 0.f, 0.f};
+                    if (tail_other) {
+                        const int j = (((pass * 2 + rr) * 2 + G) * 2 + c) * 2;
+                        const unsigned long long u0 = __hip_atomic_load(tail_other + (size_t)j * FB_THREADS,
+                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const unsigned long long u1 = __hip_atomic_load(tail_other + (size_t)(j + 1) * FB_THREADS,
+                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        o[0] = __uint_as_float((uint32_t)u0);
+                        o[1] = __uint_as_float((uint32_t)(u0 >> 32));
+                        o[2] = __uint_as_float((uint32_t)u1);
+                        o[3] = __uint_as_float((uint32_t)(u1 >> 32));
+                    }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int row = rh * 32 + rr * 16 + 4 * g + r;
                         const int col = cq * 64 + G * 32 + (i >> 3) * 16 + (i & 7) + 8 * c;
-                        ct[row * FB_CTS + col] = acc[pass * 2 + rr][G][c][r];
+                        ct[row * FB_CTS + col] = acc[pass * 2 + rr][G][c][r] + o[r];
                     }
+                }
         __syncthreads();
         if constexpr (GU) {
             // 8 rows per wave, gate and up of one 128-column block: lane l
@@ -689,6 +779,7 @@ template <int K>
 int fat_launch_k(int cb, int mt, const FatParams& p, int splits, hipStream_t st) {
     if (mt == FAT_MT_WIDE) {
         dim3 grid(p.gu ? p.n / 128 : p.n / FB_COLS, (p.M + FB_ROWS - 1) / FB_ROWS, splits);
+        if (p.tail_tiles > 0) grid = dim3(p.tail_first + 2 * p.tail_tiles, 1, 1);
         const size_t smem = fat_big_smem_bytes();
 #define EXL3_FATB(CBV, GUV)                                                                            \
     if (cb == CBV && (p.gu != 0) == GUV) {                                                             \

@@ -164,3 +164,39 @@ def test_fat_then_gemv_workspace_stays_clean():
     y = torch.ops.sglang_exl3.exl3_gemv(torch.from_numpy(xs).cuda(), *d, K, True, 1)
     torch.cuda.synchronize()
     check_close(y.float().cpu().numpy(), oracle.matmul(xs, oracle.dequant(tr, su, sv, K, 1, rtz=True)), "gemv after")
+
+
+@pytest.mark.parametrize("op", ["gemm", "gate_up"])
+def test_tail_split_repeatable(op, monkeypatch):
+    """Tail split of the wide-tile kernel (every tile of a one-round launch runs as
+    two k-halves, the first half hands its sums to the second): against the
+    oracle, bit-identical over repeated calls (the hand-off counts and flags
+    reset themselves), and close to the unsplit kernel (EXL3_FAT_TAIL=0)."""
+    # gemm: 56 x 2 tiles, enough for one k-split (smaller grids split k with
+    # fp32 atomics instead); gate/up: 2 x 2 tiles, always one split
+    m, k, K, cb = (512, 1024, 3, 1) if op == "gemm" else (300, 1024, 3, 1)
+    n = 14336 if op == "gemm" else 256
+    print(f"case: tail split {op} m={m} k={k} n={n}", flush=True)
+    x = torch.from_numpy(make_x(m, k, seed=31)).cuda()
+    if op == "gemm":
+        tr, su, sv = make_weight(k, n, K, seed=32)
+        d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
+        run = lambda: torch.ops.sglang_exl3.exl3_gemm(x, *d, K, True)
+        ref = oracle.matmul(x.cpu().numpy(), oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    else:
+        tg, su, sg = make_weight(k, n, K, seed=33)
+        tu, _, su2 = make_weight(k, n, K, seed=34)
+        d = [torch.from_numpy(v).cuda() for v in (su, tg, sg, tu, su2)]
+        run = lambda: torch.ops.sglang_exl3.exl3_gate_up_swiglu(x, *d, K, cb)
+        g = oracle.matmul(x.cpu().numpy(), oracle.dequant(tg, su, sg, K, cb, rtz=True))
+        u = oracle.matmul(x.cpu().numpy(), oracle.dequant(tu, su, su2, K, cb, rtz=True))
+        ref = oracle.swiglu(g, u, float("inf"))
+    outs = [run() for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0]), "tail split: repeated calls differ"
+    check_close(outs[0].float().cpu().numpy(), ref, f"tail split {op}")
+    monkeypatch.setenv("EXL3_FAT_TAIL", "0")
+    whole = run()
+    torch.cuda.synchronize()
+    check_close(outs[0].float().cpu().numpy(), whole.float().cpu().numpy(), f"tail split vs whole {op}")
