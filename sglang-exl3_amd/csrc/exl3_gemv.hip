@@ -187,10 +187,26 @@ bool gemv_pre_rotates(const GemvPlan& pl, int m, int experts) {
     return !pl.sk && experts == 1 && rows > 0 && m >= rows;
 }
 
-// Workspace: [counters][accumulators][partials (k-split), then the rotated
-// rows (pre-rotating calls)].
+// k-split hand-off of a single-matrix call through the fixed-point
+// accumulators (one round trip: every split rotates and adds its own partial
+// rows; gemv_kernel<.., FX = true>) instead of partial tiles, a counter and
+// a last arrival that sums them (three round trips).  Every split then pays
+// the output rotation and m x 128 adds per column block, so it pays off for
+// few rows only.  Config 2 graph-timed, fixed-point vs partials: m = 4 / 8 /
+// 12 / 16 / 32: 14.5 / 18.8-19.0 / 24.7 / 34.0 / 77.0 us vs 15.5 / 19.1 /
+// 22.8 / 30.9 / 58.1 us.  Env EXL3_GEMV_FX_ROWS overrides the row limit
+// (0: never).
+constexpr int kGemvFxRows = 8;
+
+bool gemv_fx(const GemvPlan& pl, int m, int n, int experts) {
+    return !pl.sk && experts == 1 && pl.splits > 1 && pl.splits <= SK_MAX_CONTRIB && m <= 32 &&
+           m <= env_int("EXL3_GEMV_FX_ROWS", kGemvFxRows) && (size_t)m * n * 8 <= kWsAccBytes;
+}
+
+// Workspace: [counters][accumulators][partials (k-split without the
+// fixed-point hand-off), then the rotated rows (pre-rotating calls)].
 size_t gemv_partials_bytes(const GemvPlan& pl, int m, int n, int experts) {
-    if (pl.splits <= 1) return 0;
+    if (pl.splits <= 1 || gemv_fx(pl, m, n, experts)) return 0;
     return (((size_t)(n / 128) * experts * pl.splits * (size_t)m * 128 * sizeof(float)) + 255) & ~(size_t)255;
 }
 
@@ -198,7 +214,7 @@ size_t workspace_bytes_for(const GemvPlan& pl, int m, int k, int n, int experts)
     if (pl.sk) return kWsAccOffset + (size_t)m * n * 8;
     const size_t part = gemv_partials_bytes(pl, m, n, experts);
     const size_t xr = gemv_pre_rotates(pl, m, experts) ? (size_t)m * k * 2 : 0;
-    if (part == 0 && xr == 0) return 0;
+    if (part == 0 && xr == 0) return gemv_fx(pl, m, n, experts) ? kWsAccOffset + (size_t)m * n * 8 : 0;
     return kWsScratchOffset + part + xr;
 }
 
@@ -234,6 +250,10 @@ int run_gemv(const char* fn, GemvParams p, int K, int codebook, int experts, voi
     p.nsteps = pl.nsteps;
     p.kw = pl.kw;
     p.splits = pl.splits;
+    if (gemv_fx(pl, p.m, p.n, experts) && !p.gu) {
+        p.fx = 1;
+        p.acc = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + kWsAccOffset);
+    }
     if (need) {
         EXL3_REQUIRE_CODE((size_t)(p.n / 128) * experts <= kWsMaxCounters, EXL3_ERR_UNSUPPORTED,
                           "%s: %d column blocks exceed the %zu workspace counters", fn, (p.n / 128) * experts,

@@ -61,6 +61,14 @@ struct GemvParams {
     // x holds the rows already rotated (x (.) suh, FWHT, / sqrt(128), fp16;
     // rotate_rows_kernel): the workgroups stage them as they are
     int x_rot;
+    // k-split hand-off in one round trip (fx != 0, gemv_kernel<.., FX = true>,
+    // one matrix): every split rotates and scales its own partial rows and
+    // adds them into the 64-bit fixed-point accumulators acc[m][n] (zero
+    // between calls; the format of the balanced kernel), and the add that
+    // completes an element's `splits` contributions writes its fp16 value
+    // and clears the accumulator (the output rotation is linear).
+    int fx;
+    unsigned long long* acc;
 };
 
 // Steps of weight words a wave keeps in flight.  Measured on MI355X (config 2,
@@ -321,7 +329,7 @@ __device__ __forceinline__ void decode_mfma_steps(uint32_t (&w)[D][K], const EXL
 
 // GU: the gate/up SwiGLU mode (p.gu), a separate instance so that the plain
 // GEMV carries none of its registers (71 against 199 VGPRs at K=4).
-template <int K, int CB, int MB, int NS, bool GU, bool XR = false>
+template <int K, int CB, int MB, int NS, bool GU, bool XR = false, bool FX = false>
 __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     constexpr int D = gv_depth<K>();
     extern __shared__ __align__(16) unsigned char gv_smem[];
@@ -471,10 +479,32 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
     }
     __syncthreads();
 
-    // 5. k-split reduction (last workgroup of the column block finishes).
-    // Partials travel through device-coherent (sc1) stores and loads, so the
-    // hand-off needs only "my stores completed" before the counter increment;
-    // no L2 write-back or invalidate.
+    // 5. k-split reduction.
+    if constexpr (FX) {
+        // one round trip: rotated, scaled partial rows into the fixed-point
+        // accumulators; a row's adds are checked after the next row's have
+        // been issued, so their round trips overlap
+        static_assert(!GU, "one matrix");
+        EXL3_GLOBAL __half* yf = gptr(p.y);
+        const int c0 = bx * 128 + 2 * lane;
+        const float sva = __low2float(svv) * kHadNorm, svb = __high2float(svv) * kHadNorm;
+        FxPair fx{};
+        int prow = -1;
+        for (int row = wave; row < m; row += nwaves) {
+            float a = ybuf[row * 128 + 2 * lane], b = ybuf[row * 128 + 2 * lane + 1];
+            fwht128_pair_fast(a, b, lane);
+            const FxPair cur = fx_issue_pair(p.acc + (size_t)row * n + c0, a * sva, b * svb);
+            if (prow >= 0) fx_finish_pair(fx, p.acc + (size_t)prow * n + c0, p.splits, yf + (size_t)prow * n + c0);
+            fx = cur;
+            prow = row;
+        }
+        if (prow >= 0) fx_finish_pair(fx, p.acc + (size_t)prow * n + c0, p.splits, yf + (size_t)prow * n + c0);
+        return;
+    }
+    // Otherwise the last workgroup of the column block finishes.  Partials
+    // travel through device-coherent (sc1) stores and loads, so the hand-off
+    // needs only "my stores completed" before the counter increment; no L2
+    // write-back or invalidate.
     const int nblk_n = n >> 7;
     if (p.splits > 1 || GU) {
         const size_t cblk = (size_t)e * nblk_n + bx;
@@ -571,19 +601,26 @@ int gemv_launch_k(int cb, int mb, const GemvParams& p, int experts, hipStream_t 
     dim3 grid(p.n / 128, p.splits, experts);
     const size_t smem = gemv_smem_bytes(p.m, 4 * p.nsteps * p.kw, p.kw);
     const int threads = 256 * p.kw;
-#define EXL3_GV_GU(CBV, MBV, NSV, GUV, XRV)                                                            \
-    if (cb == CBV && mb == MBV && p.nsteps == NSV && (p.gu != 0) == GUV && (p.x_rot != 0) == XRV) {    \
-        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV, GUV, XRV>);      \
+#define EXL3_GV_GU(CBV, MBV, NSV, GUV, XRV) EXL3_GV_FX(CBV, MBV, NSV, GUV, XRV, false)
+#define EXL3_GV_FX(CBV, MBV, NSV, GUV, XRV, FXV)                                                       \
+    if (cb == CBV && mb == MBV && p.nsteps == NSV && (p.gu != 0) == GUV && (p.x_rot != 0) == XRV &&    \
+        (p.fx != 0) == FXV) {                                                                          \
+        const void* fn = reinterpret_cast<const void*>(&gemv_kernel<K, CBV, MBV, NSV, GUV, XRV, FXV>); \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 gemv");                                      \
         if (lrc) return lrc;                                                                           \
-        gemv_kernel<K, CBV, MBV, NSV, GUV, XRV><<<grid, threads, smem, st>>>(p);                       \
+        gemv_kernel<K, CBV, MBV, NSV, GUV, XRV, FXV><<<grid, threads, smem, st>>>(p);                  \
         return launch_status("exl3 gemv launch");                                                      \
     }
 // gate/up mode runs with one row block (m <= 4); pre-rotated rows only in the
 // plain mode
+// one-round-trip split hand-off for one matrix up to 32 rows (pre-rotated
+// rows from 32)
 #define EXL3_GV_NS(CBV, MBV, NSV)                                                                      \
     EXL3_GV_GU(CBV, MBV, NSV, false, false) EXL3_GV_GU(CBV, MBV, NSV, false, true)                     \
-    if constexpr (MBV == 1) EXL3_GV_GU(CBV, MBV, NSV, true, false)
+    if constexpr (MBV == 1) EXL3_GV_GU(CBV, MBV, NSV, true, false)                                     \
+    if constexpr (MBV == 1) EXL3_GV_FX(CBV, MBV, NSV, false, false, true)                              \
+    if constexpr (MBV == 2) EXL3_GV_FX(CBV, MBV, NSV, false, false, true)                              \
+    if constexpr (MBV == 2) EXL3_GV_FX(CBV, MBV, NSV, false, true, true)
 #define EXL3_GV_CASE(CBV, MBV) \
     EXL3_GV_NS(CBV, MBV, 2) EXL3_GV_NS(CBV, MBV, 4) EXL3_GV_NS(CBV, MBV, 8) EXL3_GV_NS(CBV, MBV, 16)
     EXL3_GV_CASE(0, 1) EXL3_GV_CASE(0, 2) EXL3_GV_CASE(0, 4)
@@ -592,6 +629,7 @@ int gemv_launch_k(int cb, int mb, const GemvParams& p, int experts, hipStream_t 
 #undef EXL3_GV_CASE
 #undef EXL3_GV_NS
 #undef EXL3_GV_GU
+#undef EXL3_GV_FX
     set_error("exl3 gemv: no kernel for codebook %d row blocks %d steps %d", cb, mb, p.nsteps);
     return EXL3_ERR_UNSUPPORTED;
 }

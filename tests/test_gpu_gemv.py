@@ -249,6 +249,38 @@ def test_gemv_split_kernel_vs_oracle(m, k, n, K, cb):
     check_close(y.float().cpu().numpy(), ref, f"split m={m}")
 
 
+@pytest.mark.parametrize("m,fx_rows", [(4, None), (8, None), (20, "32")])
+def test_gemv_split_fixed_point_handoff(m, fx_rows):
+    """k-split kernel whose splits add their rotated partial rows into the fixed-point
+    accumulators (default up to 8 rows; 20 rows forced, two row blocks): against the
+    oracle, bit-identical over repeated calls, the workspace zero again after each
+    call, and close to the partial-tile hand-off (EXL3_GEMV_FX_ROWS=0)."""
+    k, n, K, cb = 2048, 512, 3, 1
+    print(f"case: split fixed-point gemv m={m} fx_rows={fx_rows}", flush=True)
+    env = {"EXL3_GEMV_SK": 0} if fx_rows is None else {"EXL3_GEMV_SK": 0, "EXL3_GEMV_FX_ROWS": fx_rows}
+    trellis, suh, svh = make_weight(k, n, K, seed=950 + m)
+    x = make_x(m, k, seed=951 + m)
+    xd, tr, su, sv = to_dev(x, trellis, suh, svh)
+    assert _with_env(env, lambda: _plan(m, k, n, K))[3] > 1  # several k-splits
+    L = _lib.lib()
+    need = int(_with_env(env, lambda: L.exl3_gemv_workspace_size(m, k, n, K, 1)))
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(3):
+        y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+        _with_env(env, lambda: _lib.check(
+            L.exl3_gemv(xd.data_ptr(), tr.data_ptr(), su.data_ptr(), sv.data_ptr(), y.data_ptr(), m, k, n, K, cb,
+                        ws.data_ptr(), ws.numel(), int(torch.cuda.current_stream().cuda_stream)), "exl3_gemv"))
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(ws)) == 0
+        outs.append(y)
+    for y in outs[1:]:
+        assert torch.equal(y, outs[0]), "fixed-point hand-off: repeated calls differ"
+    check_close(outs[0].float().cpu().numpy(), _oracle_ref(x, trellis, suh, svh, K, cb), f"fx m={m}")
+    tiles = _with_env({"EXL3_GEMV_SK": 0, "EXL3_GEMV_FX_ROWS": "0"}, lambda: _run_capi(xd, tr, su, sv, K, cb))
+    check_close(outs[0].float().cpu().numpy(), tiles.float().cpu().numpy(), f"fx vs tiles m={m}")
+
+
 def test_gemv_balanced_leaves_accumulators_zero():
     """Every output element's fixed-point accumulator is cleared by the workgroup that
     completes it, so the workspace's zero regions are zero after each call."""
