@@ -50,8 +50,8 @@ struct FatPlan {
 // Wide tiles (256 x 256, fat_big_kernel) above kFatNarrowMaxRows rows (env
 // EXL3_FAT_WIDE=0 turns them off); up to there the narrow kernel with 16-row
 // tiles up to 16 rows and 64-row tiles above.  k-splits for the narrow kernel
-// toward ~4 workgroups per CU (each split a whole number of FAT_CH chunks),
-// capped by the atomics they add.  The wide kernel splits only grids under 96
+// up to kFatNarrowWgs workgroups (each split a whole number of FAT_CH
+// chunks).  The wide kernel splits only grids under 96
 // workgroups (an even number of steps per split): its outputs are large, and
 // split outputs cost a zero fill plus one fp32 atomic per value and split,
 // which measured slower than leaving up to 60 % of the CUs idle.
@@ -61,6 +61,17 @@ struct FatPlan {
 // 222.6 / 129.6, 768: 227.9 / 330.7 / 131.4.  128-row narrow tiles never win
 // (kept as the EXL3_FAT_MT=128 override).
 constexpr int kFatNarrowMaxRows = 256;
+
+// k-splits of the narrow kernel: the most that keep the grid at or under
+// kFatNarrowWgs workgroups (about two per CU; more splits add partial sums
+// and shorten each workgroup's decode below what hides its latency).
+// exl3_gemm, k = 4096, K = 4, graph-timed, splits 1 / 2 / 4 / 8: n = 14336,
+// M = 16: 40.1 / 29.5 / 24.6 / 29.6 us, M = 64: 68.0 / 53.0 / 49.8 / 71.8,
+// M = 128: 69.0 / 67.5 / 89.1 / 130.0; n = 28672, M = 16: 40.2 / 37.5 / 39.6 /
+// 45.4, M = 128: 80.1 / 123.1 / 161.3 / 234.5.  Gate/up (two projections per
+// column block), n = 14336, K = 3: M = 16: 51.3 / 41.2 / 44.2 / 43.5, M = 64:
+// 103.0 / 83.8 / 87.9 / 92.3, M = 128: 117.8 / 121.9 / 121.6 / 138.6.
+constexpr long long kFatNarrowWgs = 512;
 
 bool fat_wide_allowed() {
     const char* env = getenv("EXL3_FAT_WIDE");
@@ -117,14 +128,9 @@ FatPlan plan_fat(int M, int k, int n) {
     const int fmt = env_int("EXL3_FAT_MT", 0);  // tuning override: 16, 64 or 128 rows per tile
     if (fmt == 16 || fmt == 64 || fmt == 128) pl.mt = fmt;
     const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
-    const char* fs = getenv("EXL3_FAT_SPLITS");  // tuning override (power of two)
-    const int forced = fs ? atoi(fs) : 0;
-    // every split adds M x n fp32 atomics: stop doubling before they pass 2^21
-    // (n = 28672: M = 16 takes 4 splits, M = 32 two, M = 64 one; 1.1-1.9x
-    // faster than filling the chip with splits)
-    while ((forced ? pl.splits < forced
-                   : base * pl.splits < 1024 && (long long)M * n * 2 * pl.splits <= (1LL << 21)) &&
-           pl.splits < 16 && ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+    const int forced = env_int("EXL3_FAT_SPLITS", 0);  // tuning override (power of two)
+    while ((forced ? pl.splits < forced : base * pl.splits * 2 <= kFatNarrowWgs) && pl.splits < 16 &&
+           ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
         pl.splits *= 2;
     return pl;
 }
@@ -232,7 +238,7 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
 // Gate/up SwiGLU on the MFMA kernels: the input is rotated once with the
 // shared suh into the scratch, then
 //   * up to kGateUpNarrowMaxRows rows: the narrow kernel in gate/up mode (16- or
-//     64-row tiles, k-splits toward ~4 workgroups per CU; partial tiles and one
+//     64-row tiles, k-splits up to kFatNarrowWgs workgroups; partial tiles and one
 //     counter per (column block, row tile) in the scratch);
 //   * above: the wide-tile kernel in gate/up mode (one split).
 // Config 3 (n = 14336 per projection), narrow / wide: M = 112: 109.4 / 129.1 us,
@@ -249,8 +255,9 @@ GateUpFatPlan plan_gate_up_fat(int m, int k, int n) {
     GateUpFatPlan pl{m <= 16 ? 16 : 64, 1};
     const int ksteps = k / 64;
     const long long base = 2LL * (n / 128) * ((m + pl.mt - 1) / pl.mt);
-    while (base * pl.splits * 2 <= 1024 && pl.splits < 16 && ksteps % (2 * pl.splits) == 0 &&
-           (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+    const int forced = env_int("EXL3_FAT_SPLITS", 0);  // tuning override (power of two)
+    while ((forced ? pl.splits < forced : base * pl.splits * 2 <= kFatNarrowWgs) && pl.splits < 16 &&
+           ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
         pl.splits *= 2;
     return pl;
 }
