@@ -382,33 +382,49 @@ __device__ __forceinline__ void decode_group_pairs(const uint32_t* buf, uint32_t
 // Tile row of value slot t (0..3) of quarter Q (0..3).
 __host__ __device__ constexpr int quarter_row(int Q, int t) { return 4 * (Q >> 1) + kofs(4 * (Q & 1) + t); }
 
+// mul1 raw entries: two states as the fp16 numbers 1024 + byte sum (exact,
+// bits 0x6400 + sum), two VALU ops (v_sad_u8, v_sad_hi_u8) after the hashes.
+// The value is kMul1Kinv * raw + kMul1Bias, an affine map the caller applies
+// to the product: sum_k x_k v_k = kMul1Kinv * sum_k x_k raw_k + kMul1Bias * sum_k x_k.
+constexpr float kMul1Bias = -2721792.0f / 262144.0f;  // fp16 0xc931
+__device__ __forceinline__ uint32_t mul1_raw_pair(uint32_t s0, uint32_t s1) {
+    return __builtin_amdgcn_sad_hi_u8(hash<2>(s1), 0u, __builtin_amdgcn_sad_u8(hash<2>(s0), 0u, 0x64006400u));
+}
+
 // Exact-rounding decode (dequant / decode ops): fp16 bits of two values.
-template <int K, int CB, bool RZ, int H, int C, int P>
+// RAW (mul1, round to nearest): the raw entries of mul1_raw_pair instead.
+template <int K, int CB, bool RZ, int H, int C, int P, bool RAW = false>
 __device__ __forceinline__ uint32_t frag_pair(const uint32_t* buf) {
     constexpr int e0 = 2 * P, e1 = 2 * P + 1;
     constexpr int u0 = 16 * H + (e0 & 3) + 8 * (e0 >> 2) + 4 * C;
     constexpr int u1 = 16 * H + (e1 & 3) + 8 * (e1 >> 2) + 4 * C;
     uint32_t s0 = window<K, u0>(buf), s1 = window<K, u1>(buf);
-    if constexpr (RZ) return decode2_rz<CB>(s0, s1);
-    else return decode2_rn<CB>(s0, s1);
+    if constexpr (RAW) {
+        static_assert(CB == 2 && !RZ, "raw entries: mul1, matmul side");
+        return mul1_raw_pair(s0, s1);
+    } else if constexpr (RZ) {
+        return decode2_rz<CB>(s0, s1);
+    } else {
+        return decode2_rn<CB>(s0, s1);
+    }
 }
 
-template <int K, int CB, bool RZ, int H, int C>
+template <int K, int CB, bool RZ, int H, int C, bool RAW = false>
 __device__ __forceinline__ void frag_decode(const uint32_t* buf, uint32_t* f) {
-    f[0] = frag_pair<K, CB, RZ, H, C, 0>(buf);
-    f[1] = frag_pair<K, CB, RZ, H, C, 1>(buf);
-    f[2] = frag_pair<K, CB, RZ, H, C, 2>(buf);
-    f[3] = frag_pair<K, CB, RZ, H, C, 3>(buf);
+    f[0] = frag_pair<K, CB, RZ, H, C, 0, RAW>(buf);
+    f[1] = frag_pair<K, CB, RZ, H, C, 1, RAW>(buf);
+    f[2] = frag_pair<K, CB, RZ, H, C, 2, RAW>(buf);
+    f[3] = frag_pair<K, CB, RZ, H, C, 3, RAW>(buf);
 }
 
 // Decode the 32 values of one lane's group into fp16 words frag[c][h][p]
 // (values 2p, 2p+1 of column q + 8c, run h; tile row 4h + kofs(e)).
-template <int K, int CB, bool RZ>
+template <int K, int CB, bool RZ, bool RAW = false>
 __device__ __forceinline__ void decode_group(const uint32_t* buf, uint32_t frag[2][2][4]) {
-    frag_decode<K, CB, RZ, 0, 0>(buf, frag[0][0]);
-    frag_decode<K, CB, RZ, 1, 0>(buf, frag[0][1]);
-    frag_decode<K, CB, RZ, 0, 1>(buf, frag[1][0]);
-    frag_decode<K, CB, RZ, 1, 1>(buf, frag[1][1]);
+    frag_decode<K, CB, RZ, 0, 0, RAW>(buf, frag[0][0]);
+    frag_decode<K, CB, RZ, 1, 0, RAW>(buf, frag[0][1]);
+    frag_decode<K, CB, RZ, 0, 1, RAW>(buf, frag[1][0]);
+    frag_decode<K, CB, RZ, 1, 1, RAW>(buf, frag[1][1]);
 }
 
 }  // namespace exl3

@@ -148,13 +148,21 @@ int check_fat(const char* fn, const void* a, const void* trellis, const void* ou
     return EXL3_OK;
 }
 
+// Narrow tiles of 16 or 64 rows on mul1 weights read the raw entries (two
+// VALU ops per two weights instead of four) and correct in the epilogue from
+// the rotated rows' chunk sums.  EXL3_FAT_RAW=0 turns it off (ablation).
+bool fat_raw(int cb, int mt) { return cb == 2 && (mt == 16 || mt == 64) && env_int("EXL3_FAT_RAW", 1) != 0; }
+
 // tail: tail-split tiles (unsplit wide launch with fp16 output; 0 = none),
 // their hand-off tiles at tail_part and counts / flags at tail_sync.
+// rowsum: chunk sums of a's rows, [M][k/128], for a raw-entry plan (else null).
 int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out16, const uint16_t* svh,
             const int64_t* token_idx, const uint16_t* route_w, int M, int k, int n, int K, int cb, bool zero_first,
-            hipStream_t st, int tail = 0, char* tail_part = nullptr, int* tail_sync = nullptr) {
+            hipStream_t st, int tail = 0, char* tail_part = nullptr, int* tail_sync = nullptr,
+            const float* rowsum = nullptr) {
     const FatPlan pl = plan_fat(M, k, n);
     FatParams p{};
+    if (rowsum && fat_raw(cb, pl.mt)) p.rowsum = rowsum;
     if (tail > 0) {
         p.tiles_x = n / FB_COLS;
         p.tail_tiles = tail;
@@ -194,8 +202,10 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 // Prefill path of exl3_gemm (m > gemm_gemv_rows()).  Scratch after the workspace's zeroed
 // regions (shared with the GEMV kernels, which need them to stay zero); an
 // unsplit GEMM stores fp16 straight to y.
-size_t fat_xr_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
-// [counters][accumulators][xr fp16 m*k][out fp32 m*n, only when the plan
+// xr: the rotated rows (fp16 m*k), then their chunk sums (fp32 m*k/128).
+size_t fat_xr_only_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
+size_t fat_xr_bytes(int m, int k) { return fat_xr_only_bytes(m, k) + (((size_t)m * (k / 128) * 4 + 255) & ~(size_t)255); }
+// [counters][accumulators][xr][out fp32 m*n, only when the plan
 // splits k | tail-split hand-off tiles, only for an unsplit wide launch].
 size_t fat_gemm_scratch_bytes(int m, int k, int n) {
     const FatPlan pl = plan_fat(m, k, n);
@@ -213,21 +223,24 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
     EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4), "exl3_gemm: misaligned pointer");
     __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsScratchOffset);
     float* o32 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsScratchOffset + fat_xr_bytes(m, k));
+    const FatPlan pl = plan_fat(m, k, n);
+    float* rs = fat_raw(cb, pl.mt)
+                    ? reinterpret_cast<float*>(reinterpret_cast<char*>(xr) + fat_xr_only_bytes(m, k))
+                    : nullptr;
     const long long chunks = (long long)m * (k / 128);
     rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x),
                                                                       reinterpret_cast<const __half*>(suh), xr, chunks,
-                                                                      k);
+                                                                      k, rs);
     int rc = launch_status("exl3_gemm rotate launch");
     if (rc) return rc;
-    const FatPlan pl = plan_fat(m, k, n);
     if (pl.splits == 1) {
         const int tail = pl.mt == FAT_MT_WIDE ? wide_tail_tiles(m, k, n, false) : 0;
         return run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, nullptr, reinterpret_cast<__half*>(y), svh,
                        nullptr, nullptr, m, k, n, K, cb, false, st, tail, reinterpret_cast<char*>(o32),
-                       reinterpret_cast<int*>(ws));
+                       reinterpret_cast<int*>(ws), rs);
     }
     rc = run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, o32, nullptr, svh, nullptr, nullptr, m, k, n, K, cb,
-                 true, st);
+                 true, st, 0, nullptr, nullptr, rs);
     if (rc) return rc;
     const size_t n2 = (size_t)m * n / 2;
     f32_to_f16_kernel<<<(unsigned)((n2 + 255) / 256 < 8192 ? (n2 + 255) / 256 : 8192), 256, 0, st>>>(
@@ -285,13 +298,15 @@ int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate
                       "exl3_gate_up_swiglu: %d column blocks exceed the workspace counters", n / 128);
     char* w8 = reinterpret_cast<char*>(ws);
     __half* xr = reinterpret_cast<__half*>(w8 + kWsScratchOffset);
+    float* rs = fat_raw(cb, pl.mt) ? reinterpret_cast<float*>(w8 + kWsScratchOffset + fat_xr_only_bytes(m, k)) : nullptr;
     const long long chunks = (long long)m * (k / 128);
     rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x),
                                                                       reinterpret_cast<const __half*>(suh), xr, chunks,
-                                                                      k);
+                                                                      k, rs);
     int rc = launch_status("exl3_gate_up_swiglu rotate launch");
     if (rc) return rc;
     FatParams p{};
+    p.rowsum = rs;
     p.a = xr;
     p.trellis = reinterpret_cast<const uint32_t*>(gate_trellis);
     p.svh = reinterpret_cast<const __half*>(gate_svh);

@@ -95,7 +95,20 @@ struct FatParams {
     int tail_first, tail_tiles, tiles_x;
     float* tail_part;  // [tail_tiles][FB_TAIL_FLOATS]
     int* tail_sync;    // [tail_tiles] arrival counts, then [tail_tiles] flags; zero between calls
+    // Narrow kernel on mul1 weights (fat_gemm_kernel<.., RAW = true>, plain
+    // and gate/up modes): B holds the raw entries (mul1_raw_pair) and the
+    // epilogue applies kMul1Kinv * acc + kMul1Bias * (sum of the rows' x over
+    // the k range), from rowsum[row][k/128] (rotate_rows_kernel's chunk sums).
+    const float* rowsum;
 };
+
+// Sum over chunks [c0, c0 + nc) of row `row` of rowsum (one wave).
+__device__ __forceinline__ float fat_row_sum(const float* rowsum, int nchk, int row, int c0, int nc, int lane) {
+    const float* r = rowsum + (size_t)row * nchk + c0;
+    float v = 0.f;
+    for (int c = lane; c < nc; c += 64) v += gptr(r)[c];
+    return wave_sum(v);
+}
 
 template <int K>
 __host__ __device__ constexpr int fat_depth() {
@@ -108,8 +121,9 @@ inline size_t fat_smem_bytes(int mt) {
     return a > c ? a : c;
 }
 
-template <int K, int CB, int MT>
+template <int K, int CB, int MT, bool RAW = false>
 __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
+    static_assert(!RAW || CB == 2, "raw entries: mul1");
     constexpr int RB = MT / 16;
     constexpr int D = fat_depth<K>();
     static_assert(FAT_CH % D == 0, "the register slot of a step must be static inside a chunk");
@@ -186,7 +200,7 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
             for (int j = 0; j < K; ++j) buf[1 + j] = w[d][j];
             buf[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(prev_addr, (int)buf[K]);
             uint32_t frag[2][2][4];
-            decode_group<K, CB, false>(buf, frag);
+            decode_group<K, CB, false, RAW>(buf, frag);
             if (step + D < nsteps) load_words<K>(tb + (size_t)(step + D) * step_stride, w[d]);
             const unsigned char* arow = fat_smem + (size_t)i * FAT_ROWB + (s * 4 + g) * 32;
 #pragma unroll
@@ -283,6 +297,14 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
         for (int row = cw; row < rows; row += FAT_THREADS / 64) {
             float ga = sum_splits(pg + row * 128, rs, S), gb = sum_splits(pg + row * 128 + 1, rs, S);
             float ua = sum_splits(pu + row * 128, rs, S), ub = sum_splits(pu + row * 128 + 1, rs, S);
+            if constexpr (RAW) {
+                // both projections read the same rows: one sum over all of k
+                const float sx = kMul1Bias * fat_row_sum(p.rowsum, p.k >> 7, m0 + row, 0, p.k >> 7, lane);
+                ga = ga * kMul1Kinv + sx;
+                gb = gb * kMul1Kinv + sx;
+                ua = ua * kMul1Kinv + sx;
+                ub = ub * kMul1Kinv + sx;
+            }
             fwht128_pair_fast(ga, gb, lane);
             fwht128_pair_fast(ua, ub, lane);
             ga = (ga * kHadNorm) * __low2float(svg);
@@ -302,6 +324,12 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
     const float sva = __low2float(svv), svb = __high2float(svv);
     for (int row = cw; row < rows; row += FAT_THREADS / 64) {
         float va = ct[row * 128 + 2 * lane], vb = ct[row * 128 + 2 * lane + 1];
+        if constexpr (RAW) {
+            // this split's k range: chunks kt0 / 8 .. + nsteps / 2
+            const float sx = kMul1Bias * fat_row_sum(p.rowsum, p.k >> 7, m0 + row, kt0 >> 3, nsteps >> 1, lane);
+            va = va * kMul1Kinv + sx;
+            vb = vb * kMul1Kinv + sx;
+        }
         fwht128_pair_fast(va, vb, lane);
         va = (va * kHadNorm) * sva;
         vb = (vb * kHadNorm) * svb;
@@ -795,18 +823,22 @@ int fat_launch_k(int cb, int mt, const FatParams& p, int splits, hipStream_t st)
     }
     dim3 grid((p.gu ? 2 : 1) * (p.n / 128), (p.M + mt - 1) / mt, splits);
     const size_t smem = fat_smem_bytes(mt);
-#define EXL3_FAT(CBV, MTV)                                                                             \
-    if (cb == CBV && mt == MTV) {                                                                      \
-        const void* fn = reinterpret_cast<const void*>(&fat_gemm_kernel<K, CBV, MTV>);                 \
+#define EXL3_FAT_R(CBV, MTV, RAWV)                                                                     \
+    if (cb == CBV && mt == MTV && (p.rowsum != nullptr) == RAWV) {                                     \
+        const void* fn = reinterpret_cast<const void*>(&fat_gemm_kernel<K, CBV, MTV, RAWV>);           \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 fat gemm");                                  \
         if (lrc) return lrc;                                                                           \
-        fat_gemm_kernel<K, CBV, MTV><<<grid, FAT_THREADS, smem, st>>>(p);                              \
+        fat_gemm_kernel<K, CBV, MTV, RAWV><<<grid, FAT_THREADS, smem, st>>>(p);                        \
         return launch_status("exl3 fat gemm launch");                                                  \
     }
+#define EXL3_FAT(CBV, MTV) EXL3_FAT_R(CBV, MTV, false)
 #define EXL3_FAT_CB(CBV) EXL3_FAT(CBV, 16) EXL3_FAT(CBV, 64) EXL3_FAT(CBV, 128)
     EXL3_FAT_CB(0) EXL3_FAT_CB(1) EXL3_FAT_CB(2)
+    // mul1 raw entries: 16- and 64-row tiles, plain and gate/up modes
+    if (!p.gmode) { EXL3_FAT_R(2, 16, true) EXL3_FAT_R(2, 64, true) }
 #undef EXL3_FAT_CB
 #undef EXL3_FAT
+#undef EXL3_FAT_R
     set_error("exl3 fat gemm: no kernel for codebook %d tile rows %d", cb, mt);
     return EXL3_ERR_UNSUPPORTED;
 }

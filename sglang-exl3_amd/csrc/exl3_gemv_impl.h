@@ -576,8 +576,10 @@ namespace {
 // Input rotation of a row batch: xr = fp16( H(x (.) suh) / sqrt(128) ), one
 // wave per 128-wide chunk (feeds the k-split GEMV's pre-rotated mode and the
 // MFMA GEMM).
+// rs (optional): the sum of each chunk's 128 rotated fp16 values, [row][k/128]
+// (the mul1 raw-entry GEMM's affine correction).
 __global__ __launch_bounds__(256) void rotate_rows_kernel(const __half* x, const __half* suh, __half* xr,
-                                                          long long chunks, int k) {
+                                                          long long chunks, int k, float* rs = nullptr) {
     const long long chunk = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (chunk >= chunks) return;
     const int lane = threadIdx.x & 63, per_row = k >> 7;
@@ -586,7 +588,12 @@ __global__ __launch_bounds__(256) void rotate_rows_kernel(const __half* x, const
     const __half2 pr = __hmul2(ld_h2(gptr(x) + (size_t)row * k + c), ld_h2(gptr(suh) + c));
     float a = __low2float(pr), b = __high2float(pr);
     fwht128_pair_fast(a, b, lane);
-    st_h2(gptr(xr) + (size_t)row * k + c, h2_rn(a * kHadNorm, b * kHadNorm));
+    const __half2 o = h2_rn(a * kHadNorm, b * kHadNorm);
+    st_h2(gptr(xr) + (size_t)row * k + c, o);
+    if (rs) {
+        const float t = wave_sum(__low2float(o) + __high2float(o));
+        if (lane == 0) gptr(rs)[chunk] = t;
+    }
 }
 }  // namespace
 

@@ -200,3 +200,37 @@ def test_tail_split_repeatable(op, monkeypatch):
     whole = run()
     torch.cuda.synchronize()
     check_close(outs[0].float().cpu().numpy(), whole.float().cpu().numpy(), f"tail split vs whole {op}")
+
+
+@pytest.mark.parametrize("op,m", [("gemm", 16), ("gemm", 48), ("gate_up", 16), ("gate_up", 48)])
+def test_mul1_raw_entries(op, m, monkeypatch):
+    """Narrow tiles on mul1 weights read raw entries (1024 + byte sum, no affine
+    step) and correct in the epilogue with kinv * acc + bias * (row sum of the
+    rotated x over the split's k range).  k = 14336 (112 chunk sums per row,
+    split over several k ranges): against the oracle and close to the decoded
+    path (EXL3_FAT_RAW=0)."""
+    k, n, K, cb = 14336, 256, 3, 2
+    print(f"case: raw mul1 {op} m={m} k={k} n={n}", flush=True)
+    x = torch.from_numpy(make_x(m, k, seed=51 + m)).cuda()
+    if op == "gemm":
+        tr, su, sv = make_weight(k, n, K, seed=52)
+        d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
+        run = lambda: torch.ops.sglang_exl3.exl3_gemm(x, *d, K, False)
+        ref = oracle.matmul(x.cpu().numpy(), oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    else:
+        tg, su, sg = make_weight(k, n, K, seed=53)
+        tu, _, su2 = make_weight(k, n, K, seed=54)
+        # svh / 16 keeps silu(g) * u inside fp16 at this k
+        sg, su2 = (sg / 16).astype(np.float16), (su2 / 16).astype(np.float16)
+        d = [torch.from_numpy(v).cuda() for v in (su, tg, sg, tu, su2)]
+        run = lambda: torch.ops.sglang_exl3.exl3_gate_up_swiglu(x, *d, K, cb)
+        g = oracle.matmul(x.cpu().numpy(), oracle.dequant(tg, su, sg, K, cb, rtz=True))
+        u = oracle.matmul(x.cpu().numpy(), oracle.dequant(tu, su, su2, K, cb, rtz=True))
+        ref = oracle.swiglu(g, u, float("inf"))
+    raw = run()
+    torch.cuda.synchronize()
+    check_close(raw.float().cpu().numpy(), ref, f"raw mul1 {op} m={m}")
+    monkeypatch.setenv("EXL3_FAT_RAW", "0")
+    dec = run()
+    torch.cuda.synchronize()
+    check_close(raw.float().cpu().numpy(), dec.float().cpu().numpy(), f"raw vs decoded {op} m={m}")
