@@ -166,22 +166,23 @@ def test_fat_then_gemv_workspace_stays_clean():
     check_close(y.float().cpu().numpy(), oracle.matmul(xs, oracle.dequant(tr, su, sv, K, 1, rtz=True)), "gemv after")
 
 
+@pytest.mark.parametrize("cb", [1, 2])
 @pytest.mark.parametrize("op", ["gemm", "gate_up"])
-def test_tail_split_repeatable(op, monkeypatch):
+def test_tail_split_repeatable(op, cb, monkeypatch):
     """Tail split of the wide-tile kernel (every tile of a one-round launch runs as
     two k-halves, the first half hands its sums to the second): against the
     oracle, bit-identical over repeated calls (the hand-off counts and flags
     reset themselves), and close to the unsplit kernel (EXL3_FAT_TAIL=0)."""
     # gemm: 56 x 2 tiles, enough for one k-split (smaller grids split k with
     # fp32 atomics instead); gate/up: 2 x 2 tiles, always one split
-    m, k, K, cb = (512, 1024, 3, 1) if op == "gemm" else (300, 1024, 3, 1)
+    m, k, K = (512, 1024, 3) if op == "gemm" else (300, 1024, 3)
     n = 14336 if op == "gemm" else 256
-    print(f"case: tail split {op} m={m} k={k} n={n}", flush=True)
+    print(f"case: tail split {op} m={m} k={k} n={n} cb={cb}", flush=True)
     x = torch.from_numpy(make_x(m, k, seed=31)).cuda()
     if op == "gemm":
         tr, su, sv = make_weight(k, n, K, seed=32)
         d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
-        run = lambda: torch.ops.sglang_exl3.exl3_gemm(x, *d, K, True)
+        run = lambda: torch.ops.sglang_exl3.exl3_gemm(x, *d, K, cb == 1)
         ref = oracle.matmul(x.cpu().numpy(), oracle.dequant(tr, su, sv, K, cb, rtz=True))
     else:
         tg, su, sg = make_weight(k, n, K, seed=33)
@@ -202,13 +203,16 @@ def test_tail_split_repeatable(op, monkeypatch):
     check_close(outs[0].float().cpu().numpy(), whole.float().cpu().numpy(), f"tail split vs whole {op}")
 
 
-@pytest.mark.parametrize("op,m", [("gemm", 16), ("gemm", 48), ("gate_up", 16), ("gate_up", 48)])
+@pytest.mark.parametrize("op,m", [("gemm", 16), ("gemm", 48), ("gemm", 300), ("gate_up", 16), ("gate_up", 48),
+                                  ("gate_up", 200)])
 def test_mul1_raw_entries(op, m, monkeypatch):
-    """Narrow tiles on mul1 weights read raw entries (1024 + byte sum, no affine
-    step) and correct in the epilogue with kinv * acc + bias * (row sum of the
-    rotated x over the split's k range).  k = 14336 (112 chunk sums per row,
-    split over several k ranges): against the oracle and close to the decoded
-    path (EXL3_FAT_RAW=0)."""
+    """Narrow MFMA tiles on mul1 weights read raw entries (1024 + byte sum, no
+    affine step) and correct in the epilogue with kinv * acc + bias * (row sum
+    of the rotated x over the split's k range).  k = 14336 (112 chunk sums per
+    row), narrow tiles with k-splits (m = 16, 48): against the oracle and close
+    to the decoded path (EXL3_FAT_RAW=0).  The wide tiles (gemm m = 300: 16
+    fp32-atomic k-splits; gate/up m = 200: tail-split k-halves) decode values
+    and are checked at the same k."""
     k, n, K, cb = 14336, 256, 3, 2
     print(f"case: raw mul1 {op} m={m} k={k} n={n}", flush=True)
     x = torch.from_numpy(make_x(m, k, seed=51 + m)).cuda()
