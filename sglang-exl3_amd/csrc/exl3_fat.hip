@@ -68,9 +68,8 @@ constexpr int kFatNarrowMaxRows = 256;
 // exl3_gemm, k = 4096, K = 4, graph-timed, splits 1 / 2 / 4 / 8: n = 14336,
 // M = 16: 40.1 / 29.5 / 24.6 / 29.6 us, M = 64: 68.0 / 53.0 / 49.8 / 71.8,
 // M = 128: 69.0 / 67.5 / 89.1 / 130.0; n = 28672, M = 16: 40.2 / 37.5 / 39.6 /
-// 45.4, M = 128: 80.1 / 123.1 / 161.3 / 234.5.  Gate/up (two projections per
-// column block), n = 14336, K = 3: M = 16: 51.3 / 41.2 / 44.2 / 43.5, M = 64:
-// 103.0 / 83.8 / 87.9 / 92.3, M = 128: 117.8 / 121.9 / 121.6 / 138.6.
+// 45.4, M = 128: 80.1 / 123.1 / 161.3 / 234.5.  (Gate/up mode has its own rule,
+// plan_gate_up_fat.)
 constexpr long long kFatNarrowWgs = 512;
 
 bool fat_wide_allowed() {
@@ -251,12 +250,20 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
 // Gate/up SwiGLU on the MFMA kernels: the input is rotated once with the
 // shared suh into the scratch, then
 //   * up to kGateUpNarrowMaxRows rows: the narrow kernel in gate/up mode (16- or
-//     64-row tiles, k-splits up to kFatNarrowWgs workgroups; partial tiles and one
-//     counter per (column block, row tile) in the scratch);
-//   * above: the wide-tile kernel in gate/up mode (one split).
-// Config 3 (n = 14336 per projection), narrow / wide: M = 112: 109.4 / 129.1 us,
-// 128: 122.9 / 129.3, 144: 155.0 / 129.4, 256: 227.9 / 133.3.
+//     64-row tiles; partial tiles and one counter per (column block, row tile)
+//     in the scratch);
+//   * above: the wide-tile kernel in gate/up mode (one split, tail split).
+// k-splits of the narrow kernel: the most that keep the grid within 1.25 rounds
+// of resident workgroups (CUs x waves per SIMD: 4 for 16-row tiles, 3 for 64)
+// and, on 64-row tiles, at least 32 steps per split (shorter splits spend more
+// on the hand-off and epilogue than the extra workgroups win).  Config 3
+// (n = 14336 per projection, k = 4096), graph-timed, narrow splits 1 / 2 / 4 /
+// 8: M = 16: 41.9 / 32.1 / 30.1 / 30.1 us, 32: 59.0 / 43.9 / 44.7 / 46.6, 64:
+// 83.3 / 60.6 / 63.6 / 69.0, 96: 84.2 / 72.8 / 78.5 / 89.5, 128: 92.8 / 94.0 /
+// 87.9 / 103.7, 160: 97.9 / 102.3 / 109.8 / 125.2, 192: 110.0 / 115.3 / 118.4
+// / 137.5; wide tiles M = 160 / 192 / 256: 97.8 / 97.0 / 97.9.
 constexpr int kGateUpNarrowMaxRows = 128;
+constexpr int kGateUpMinSplitSteps = 32;
 
 // Scratch: [counters][accumulators][xr fp16 m*k][partials, narrow only].
 struct GateUpFatPlan {
@@ -268,9 +275,12 @@ GateUpFatPlan plan_gate_up_fat(int m, int k, int n) {
     GateUpFatPlan pl{m <= 16 ? 16 : 64, 1};
     const int ksteps = k / 64;
     const long long base = 2LL * (n / 128) * ((m + pl.mt - 1) / pl.mt);
+    const long long resident = (long long)fat_cus() * (pl.mt == 16 ? 4 : 3);
+    const int min_steps = pl.mt == 16 ? 0 : kGateUpMinSplitSteps;
     const int forced = env_int("EXL3_FAT_SPLITS", 0);  // tuning override (power of two)
-    while ((forced ? pl.splits < forced : base * pl.splits * 2 <= kFatNarrowWgs) && pl.splits < 16 &&
-           ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+    while ((forced ? pl.splits < forced
+                   : base * pl.splits * 8 <= resident * 5 && ksteps / (2 * pl.splits) >= min_steps) &&
+           pl.splits < 16 && ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
         pl.splits *= 2;
     return pl;
 }

@@ -121,8 +121,10 @@ inline size_t fat_smem_bytes(int mt) {
     return a > c ? a : c;
 }
 
+// 16-row tiles: four waves per SIMD (123-128 VGPRs, no spills); the wider
+// tiles' accumulators leave room for three.
 template <int K, int CB, int MT, bool RAW = false>
-__global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
+__global__ __launch_bounds__(FAT_THREADS, MT == 16 ? 4 : 1) void fat_gemm_kernel(FatParams p) {
     static_assert(!RAW || CB == 2, "raw entries: mul1");
     constexpr int RB = MT / 16;
     constexpr int D = fat_depth<K>();
@@ -295,8 +297,12 @@ __global__ __launch_bounds__(FAT_THREADS) void fat_gemm_kernel(FatParams p) {
         const __half2 svg = ld_h2(gptr(p.svh) + c0), svu = ld_h2(gptr(p.svh2) + c0);
         const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
         for (int row = cw; row < rows; row += FAT_THREADS / 64) {
-            float ga = sum_splits(pg + row * 128, rs, S), gb = sum_splits(pg + row * 128 + 1, rs, S);
-            float ua = sum_splits(pu + row * 128, rs, S), ub = sum_splits(pu + row * 128 + 1, rs, S);
+            // both columns of both projections in groups of 8 splits (32
+            // values in flight: the kernel's register budget is set here)
+            const float* const src[2] = {pg + row * 128, pu + row * 128};
+            float2 gu2[2];
+            sum_splits2<2>(src, rs, S, gu2);
+            float ga = gu2[0].x, gb = gu2[0].y, ua = gu2[1].x, ub = gu2[1].y;
             if constexpr (RAW) {
                 // both projections read the same rows: one sum over all of k
                 const float sx = kMul1Bias * fat_row_sum(p.rowsum, p.k >> 7, m0 + row, 0, p.k >> 7, lane);
