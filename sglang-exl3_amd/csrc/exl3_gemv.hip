@@ -333,11 +333,11 @@ int run_gate_up_gemv(const uint16_t* x, const uint16_t* suh, const int16_t* gt, 
 
 // Rows up to which exl3_gate_up_swiglu runs the GEMV kernel; above, the input
 // is rotated once and the MFMA kernels run in gate/up mode.  Graph-timed on
-// config 3 (k = 4096, n = 2 x 14336, K = 3): m = 1 / 2 / 4: GEMV 26.7 / 28.7 /
-// 32.7 us against 33.5 / 34.2 / 34.4 us; m = 8 / 16 / 64: 41.5 / 58.8 / 298 us
-// against 37.6 / 44.3 / 90.8 us (the GEMV workgroups each re-rotate all m
+// config 3 (k = 4096, n = 2 x 14336, K = 3), GEMV / MFMA: m = 1 / 2 / 3 / 4 /
+// 8: 21.1 / 22.9 / 24.4-24.5 / 26.4 / 27.4 us against 24.5-25.3 / 24.9-25.1 /
+// 24.8-25.1 / 25.1-25.5 / 27.1 us (the GEMV workgroups each re-rotate all m
 // input rows of their k range).
-constexpr int kGateUpMaxGemvRows = 4;
+constexpr int kGateUpMaxGemvRows = 3;
 
 size_t fat_gate_up_scratch_bytes(int m, int k, int n);
 int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis, const uint16_t* gate_svh,
