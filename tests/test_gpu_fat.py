@@ -1,5 +1,5 @@
 """GPU parity of the many-row MFMA GEMM: exl3_fat_gemm / exl3_fat_gemm_scatter
-(rotated fp16 input, fp32 output) and exl3_gemm's prefill path (m ≥ 16),
+(rotated fp16 input, fp32 output) and exl3_gemm's prefill path (m ≥ 12),
 against the oracle (bar: max-abs-err <= 2e-2 * rms(ref), cosine >= 0.9999)."""
 
 import numpy as np

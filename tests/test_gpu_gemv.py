@@ -110,7 +110,7 @@ def test_gemv_zero_trellis_closed_form():
         assert np.abs(y[:, mask]).max() <= 1e-3 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("m", [1, 16, 64, 130])
+@pytest.mark.parametrize("m", [1, 11, 12, 16, 64, 130])
 def test_gemm_any_rows(m):
     print(f"case: gemm m={m}", flush=True)
     k, n, K = 512, 256, 3
