@@ -254,16 +254,17 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
 //     in the scratch);
 //   * above: the wide-tile kernel in gate/up mode (one split, tail split).
 // k-splits of the narrow kernel: the most that keep the grid within 1.25 rounds
-// of resident workgroups (CUs x waves per SIMD: 4 for 16-row tiles, 3 for 64)
-// and, on 64-row tiles, at least 32 steps per split (shorter splits spend more
-// on the hand-off and epilogue than the extra workgroups win).  Config 3
-// (n = 14336 per projection, k = 4096), graph-timed, narrow splits 1 / 2 / 4 /
-// 8: M = 16: 41.9 / 32.1 / 30.1 / 30.1 us, 32: 59.0 / 43.9 / 44.7 / 46.6, 64:
-// 83.3 / 60.6 / 63.6 / 69.0, 96: 84.2 / 72.8 / 78.5 / 89.5, 128: 92.8 / 94.0 /
-// 87.9 / 103.7, 160: 97.9 / 102.3 / 109.8 / 125.2, 192: 110.0 / 115.3 / 118.4
-// / 137.5; wide tiles M = 160 / 192 / 256: 97.8 / 97.0 / 97.9.
-constexpr int kGateUpNarrowMaxRows = 128;
-constexpr int kGateUpMinSplitSteps = 32;
+// of resident workgroups (CUs x waves per SIMD: 6 for 16-row tiles, set by
+// their ~75 VGPRs, 4 for 64-row tiles, set by their LDS) and at least 16 steps
+// per split (shorter splits spend more on the hand-off and epilogue than the
+// extra workgroups win).  Config 3 (n = 14336 per projection, k = 4096),
+// graph-timed, narrow splits 1 / 2 / 4 / 8: M = 16: 41.1 / 31.1 / 29.7 / 31.8
+// us, 32: 57.0 / 42.0 / 39.7 / 43.2, 64: 80.1 / 57.1 / 56.6 / 64.4, 96: 80.6 /
+// 68.5 / 74.1 / 88.6, 128: 89.0 / 79.2 / 81.0 / 96.8, 160: 93.7 / 106.0 / 98.7 /
+// 118.0, 192: 106.8 / 110.9 / 109.8 / 132.8; wide tiles M = 160 / 192 / 256:
+// 98.2 / 96.8 / 97.7.
+constexpr int kGateUpNarrowMaxRows = 160;
+constexpr int kGateUpMinSplitSteps = 16;
 
 // Scratch: [counters][accumulators][xr fp16 m*k][partials, narrow only].
 struct GateUpFatPlan {
@@ -275,8 +276,8 @@ GateUpFatPlan plan_gate_up_fat(int m, int k, int n) {
     GateUpFatPlan pl{m <= 16 ? 16 : 64, 1};
     const int ksteps = k / 64;
     const long long base = 2LL * (n / 128) * ((m + pl.mt - 1) / pl.mt);
-    const long long resident = (long long)fat_cus() * (pl.mt == 16 ? 4 : 3);
-    const int min_steps = pl.mt == 16 ? 0 : kGateUpMinSplitSteps;
+    const long long resident = (long long)fat_cus() * (pl.mt == 16 ? 6 : 4);
+    const int min_steps = kGateUpMinSplitSteps;
     const int forced = env_int("EXL3_FAT_SPLITS", 0);  // tuning override (power of two)
     while ((forced ? pl.splits < forced
                    : base * pl.splits * 8 <= resident * 5 && ksteps / (2 * pl.splits) >= min_steps) &&

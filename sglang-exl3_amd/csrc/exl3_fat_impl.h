@@ -121,10 +121,10 @@ inline size_t fat_smem_bytes(int mt) {
     return a > c ? a : c;
 }
 
-// 16-row tiles: four waves per SIMD (123-128 VGPRs, no spills); the wider
-// tiles' accumulators leave room for three.
+// At least four waves per SIMD for 16- and 64-row tiles (75-80 / 90 VGPRs at
+// K = 3, no spills: 6 / 5 waves; 64-row tiles are held to 4 by their LDS).
 template <int K, int CB, int MT, bool RAW = false>
-__global__ __launch_bounds__(FAT_THREADS, MT == 16 ? 4 : 1) void fat_gemm_kernel(FatParams p) {
+__global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel(FatParams p) {
     static_assert(!RAW || CB == 2, "raw entries: mul1");
     constexpr int RB = MT / 16;
     constexpr int D = fat_depth<K>();
@@ -297,11 +297,12 @@ __global__ __launch_bounds__(FAT_THREADS, MT == 16 ? 4 : 1) void fat_gemm_kernel
         const __half2 svg = ld_h2(gptr(p.svh) + c0), svu = ld_h2(gptr(p.svh2) + c0);
         const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
         for (int row = cw; row < rows; row += FAT_THREADS / 64) {
-            // both columns of both projections in groups of 8 splits (32
-            // values in flight: the kernel's register budget is set here)
+            // both columns of both projections in groups of 4 splits (16
+            // values and 8 addresses in flight: with 8 splits per group this
+            // loop set the kernel's register budget)
             const float* const src[2] = {pg + row * 128, pu + row * 128};
             float2 gu2[2];
-            sum_splits2<2>(src, rs, S, gu2);
+            sum_splits2<2, 4>(src, rs, S, gu2);
             float ga = gu2[0].x, gb = gu2[0].y, ua = gu2[1].x, ub = gu2[1].y;
             if constexpr (RAW) {
                 // both projections read the same rows: one sum over all of k

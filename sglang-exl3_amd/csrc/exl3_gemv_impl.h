@@ -122,23 +122,23 @@ __device__ __forceinline__ float sum_splits(const float* p, size_t stride, int S
 }
 
 // Two adjacent columns of sum_splits (64-bit loads), for `np` projections at
-// once (pointer p[j], j < np), in groups of 8 splits: one round trip for up
-// to 8 splits with at most 2 * 8 * np values in flight.
-template <int NP>
+// once (pointer p[j], j < np), in groups of G splits: one round trip for up
+// to G splits with at most 2 * G * np values in flight.
+template <int NP, int G = 8>
 __device__ __forceinline__ void sum_splits2(const float* const (&p)[NP], size_t stride, int S, float2 (&out)[NP]) {
 #pragma unroll
     for (int j = 0; j < NP; ++j) out[j] = make_float2(0.f, 0.f);
-    for (int s0 = 0; s0 < S; s0 += 8) {
-        float2 v[NP][8];
+    for (int s0 = 0; s0 < S; s0 += G) {
+        float2 v[NP][G];
 #pragma unroll
         for (int j = 0; j < NP; ++j)
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+            for (int t = 0; t < G; ++t)
                 v[j][t] = (s0 + t < S) ? coherent_load2(p[j] + (size_t)(s0 + t) * stride) : make_float2(0.f, 0.f);
 #pragma unroll
         for (int j = 0; j < NP; ++j)
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+            for (int t = 0; t < G; ++t)
                 if (s0 + t < S) {
                     out[j].x += v[j][t].x;
                     out[j].y += v[j][t].y;
