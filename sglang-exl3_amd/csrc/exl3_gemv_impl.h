@@ -536,7 +536,9 @@ __global__ __launch_bounds__(GV_MAX_THREADS) void gemv_kernel(GemvParams p) {
             for (int row = wave; row < m; row += nwaves) {
                 const float* const src[2] = {pg + row * 128 + 2 * lane, pu + row * 128 + 2 * lane};
                 float2 gu2[2];
-                sum_splits2<2>(src, rstride, p.splits, gu2);
+                // groups of 4 splits: 8 splits per group held this instance
+                // at 116 VGPRs (4 waves per SIMD) against 68 (7)
+                sum_splits2<2, 4>(src, rstride, p.splits, gu2);
                 float ga = gu2[0].x, gb = gu2[0].y, ua = gu2[1].x, ub = gu2[1].y;
                 fwht128_pair_fast(ga, gb, lane);
                 fwht128_pair_fast(ua, ub, lane);
