@@ -147,10 +147,13 @@ int check_fat(const char* fn, const void* a, const void* trellis, const void* ou
     return EXL3_OK;
 }
 
-// Narrow tiles of 16 or 64 rows on mul1 weights read the raw entries (two
-// VALU ops per two weights instead of four) and correct in the epilogue from
-// the rotated rows' chunk sums.  EXL3_FAT_RAW=0 turns it off (ablation).
-bool fat_raw(int cb, int mt) { return cb == 2 && (mt == 16 || mt == 64) && env_int("EXL3_FAT_RAW", 1) != 0; }
+// Narrow 16-row tiles on mul1 weights read the raw entries (two VALU ops per
+// two weights instead of four) and correct in the epilogue from the rotated
+// rows' chunk sums.  Graph-timed, raw / decoded: config 3 gate/up M = 16:
+// 29.3 / 31.6 us, exl3_gemm k = 4096, n = 14336, M = 16: 22.7 / 23.2 us; on
+// 64-row tiles the per-row sums cost more than the decode saves (gate/up
+// M = 64: 55.8 / 53.7 us).  EXL3_FAT_RAW=0 turns it off (ablation).
+bool fat_raw(int cb, int mt) { return cb == 2 && mt == 16 && env_int("EXL3_FAT_RAW", 1) != 0; }
 
 // tail: tail-split tiles (unsplit wide launch with fp16 output; 0 = none),
 // their hand-off tiles at tail_part and counts / flags at tail_sync.

@@ -841,8 +841,8 @@ int fat_launch_k(int cb, int mt, const FatParams& p, int splits, hipStream_t st)
 #define EXL3_FAT(CBV, MTV) EXL3_FAT_R(CBV, MTV, false)
 #define EXL3_FAT_CB(CBV) EXL3_FAT(CBV, 16) EXL3_FAT(CBV, 64) EXL3_FAT(CBV, 128)
     EXL3_FAT_CB(0) EXL3_FAT_CB(1) EXL3_FAT_CB(2)
-    // mul1 raw entries: 16- and 64-row tiles, plain and gate/up modes
-    if (!p.gmode) { EXL3_FAT_R(2, 16, true) EXL3_FAT_R(2, 64, true) }
+    // mul1 raw entries: 16-row tiles, plain and gate/up modes
+    if (!p.gmode) { EXL3_FAT_R(2, 16, true) }
 #undef EXL3_FAT_CB
 #undef EXL3_FAT
 #undef EXL3_FAT_R

@@ -206,13 +206,13 @@ def test_tail_split_repeatable(op, cb, monkeypatch):
 @pytest.mark.parametrize("op,m", [("gemm", 16), ("gemm", 48), ("gemm", 300), ("gate_up", 16), ("gate_up", 48),
                                   ("gate_up", 200)])
 def test_mul1_raw_entries(op, m, monkeypatch):
-    """Narrow MFMA tiles on mul1 weights read raw entries (1024 + byte sum, no
-    affine step) and correct in the epilogue with kinv * acc + bias * (row sum
-    of the rotated x over the split's k range).  k = 14336 (112 chunk sums per
-    row), narrow tiles with k-splits (m = 16, 48): against the oracle and close
-    to the decoded path (EXL3_FAT_RAW=0).  The wide tiles (gemm m = 300: 16
-    fp32-atomic k-splits; gate/up m = 200: tail-split k-halves) decode values
-    and are checked at the same k."""
+    """Narrow 16-row MFMA tiles on mul1 weights read raw entries (1024 + byte
+    sum, no affine step) and correct in the epilogue with kinv * acc + bias *
+    (row sum of the rotated x over the split's k range).  k = 14336 (112 chunk
+    sums per row), 16-row tiles with k-splits (m = 16): against the oracle and
+    close to the decoded path (EXL3_FAT_RAW=0).  The 64-row tiles (m = 48) and
+    the wide tiles (gemm m = 300: 16 fp32-atomic k-splits; gate/up m = 200:
+    tail-split k-halves) decode values and are checked at the same k."""
     k, n, K, cb = 14336, 256, 3, 2
     print(f"case: raw mul1 {op} m={m} k={k} n={n}", flush=True)
     x = torch.from_numpy(make_x(m, k, seed=51 + m)).cuda()
