@@ -502,10 +502,12 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
         // 6. epilogue, one row per wave, 2 columns per lane; split partials
-        //    of a row are all requested before the first add (one round
-        //    trip) and summed in split order
+        //    of a row are requested in groups of 4 splits before their adds
+        //    (one round trip per group) and summed in split order.  Groups of
+        //    8 held the gate/up variants at the 128-VGPR cap with spills
+        //    (102 VGPRs and none with 4).
         auto sum_rows = [&](int np, int crow, float2* out) {
-            constexpr int G = 8;
+            constexpr int G = 4;
             for (int s0 = 0; s0 < S; s0 += G) {
                 float2 v[2][G];
 #pragma unroll
