@@ -155,15 +155,32 @@ int check_fat(const char* fn, const void* a, const void* trellis, const void* ou
 // M = 64: 55.8 / 53.7 us).  EXL3_FAT_RAW=0 turns it off (ablation).
 bool fat_raw(int cb, int mt) { return cb == 2 && mt == 16 && env_int("EXL3_FAT_RAW", 1) != 0; }
 
+// Narrow plans with k-splits and fp16 output hand partial tiles to the last
+// split of each (column block, row tile) instead of adding fp32 atomically
+// into a zero-filled buffer that a third launch converts.  EXL3_FAT_HANDOFF=0
+// keeps the atomic path (ablation).
+bool fat_handoff(const FatPlan& pl, int m, int n) {
+    return pl.splits > 1 && pl.mt != FAT_MT_WIDE &&
+           (size_t)(n / 128) * (size_t)((m + pl.mt - 1) / pl.mt) <= kWsMaxCounters &&
+           env_int("EXL3_FAT_HANDOFF", 1) != 0;
+}
+
 // tail: tail-split tiles (unsplit wide launch with fp16 output; 0 = none),
 // their hand-off tiles at tail_part and counts / flags at tail_sync.
 // rowsum: chunk sums of a's rows, [M][k/128], for a raw-entry plan (else null).
+// partials / counters: the split hand-off's partial tiles and counters
+// (fat_handoff plans with fp16 output; else null).
 int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out16, const uint16_t* svh,
             const int64_t* token_idx, const uint16_t* route_w, int M, int k, int n, int K, int cb, bool zero_first,
             hipStream_t st, int tail = 0, char* tail_part = nullptr, int* tail_sync = nullptr,
-            const float* rowsum = nullptr) {
+            const float* rowsum = nullptr, float* partials = nullptr, int* counters = nullptr) {
     const FatPlan pl = plan_fat(M, k, n);
     FatParams p{};
+    if (partials && pl.splits > 1) {
+        p.handoff = 1;
+        p.partials = partials;
+        p.counters = counters;
+    }
     if (rowsum && fat_raw(cb, pl.mt)) p.rowsum = rowsum;
     if (tail > 0) {
         p.tiles_x = n / FB_COLS;
@@ -184,7 +201,7 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
     p.n = n;
     p.ksteps = k / 64 / pl.splits;
     const bool scatter = token_idx != nullptr;
-    p.accumulate = (scatter || pl.splits > 1) ? 1 : 0;
+    p.accumulate = (scatter || (pl.splits > 1 && !p.handoff)) ? 1 : 0;
     if (out16 && p.accumulate) {
         set_error("exl3 fat gemm: fp16 output needs a single k-split");
         return EXL3_ERR_UNSUPPORTED;
@@ -207,13 +224,15 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 // xr: the rotated rows (fp16 m*k), then their chunk sums (fp32 m*k/128).
 size_t fat_xr_only_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
 size_t fat_xr_bytes(int m, int k) { return fat_xr_only_bytes(m, k) + (((size_t)m * (k / 128) * 4 + 255) & ~(size_t)255); }
-// [counters][accumulators][xr][out fp32 m*n, only when the plan
-// splits k | tail-split hand-off tiles, only for an unsplit wide launch].
+// [counters][accumulators][xr][split partial tiles S*m*n fp32 (narrow
+// hand-off) | out fp32 m*n (wide plan with k-splits) | tail-split hand-off
+// tiles (unsplit wide launch)].
 size_t fat_gemm_scratch_bytes(int m, int k, int n) {
     const FatPlan pl = plan_fat(m, k, n);
     const bool split = pl.splits > 1;
     const size_t tail = (!split && pl.mt == FAT_MT_WIDE) ? fat_tail_bytes(wide_tail_tiles(m, k, n, false)) : 0;
-    return kWsScratchOffset + fat_xr_bytes(m, k) + (split ? (size_t)m * n * 4 : tail);
+    const size_t out = fat_handoff(pl, m, n) ? (size_t)pl.splits * m * n * 4 : (size_t)m * n * 4;
+    return kWsScratchOffset + fat_xr_bytes(m, k) + (split ? out : tail);
 }
 
 int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh, uint16_t* y,
@@ -241,6 +260,10 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
                        nullptr, nullptr, m, k, n, K, cb, false, st, tail, reinterpret_cast<char*>(o32),
                        reinterpret_cast<int*>(ws), rs);
     }
+    if (fat_handoff(pl, m, n))
+        return run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, nullptr, reinterpret_cast<__half*>(y), svh,
+                       nullptr, nullptr, m, k, n, K, cb, false, st, 0, nullptr, nullptr, rs, o32,
+                       reinterpret_cast<int*>(ws));
     rc = run_fat(reinterpret_cast<const uint16_t*>(xr), trellis, o32, nullptr, svh, nullptr, nullptr, m, k, n, K, cb,
                  true, st, 0, nullptr, nullptr, rs);
     if (rc) return rc;

@@ -68,8 +68,13 @@ struct FatParams {
     const uint32_t* trellis2;
     const __half* svh2;
     float limit;  // <= 0 or inf: no clamp
-    float* partials;  // [n/128][2][S][M][128] (narrow gate/up mode)
+    float* partials;  // [n/128][2][S][M][128] (narrow gate/up mode), [n/128][S][M][128] (handoff)
     int* counters;    // [n/128][row tiles], zero between calls
+    // fat_gemm_kernel plain mode with k-splits and fp16 output (handoff != 0):
+    // the same partial-tile hand-off with one projection; the last of the S
+    // arrivals of a (column block, row tile) applies the epilogue and stores
+    // out16 (deterministic, no fp32 atomics, zero fill or conversion pass).
+    int handoff;
     // Grouped mode of fat_gemm_kernel (MoE prefill), gmode != 0: blockIdx.y
     // indexes `tiles` (tiles at or past *ntiles exit at once, so the grid is
     // static), `a` holds the rows in compact order, and the weights are the
@@ -273,13 +278,15 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
         }
         return;
     }
-    if (p.gu) {
-        // hand-off of the gate/up mode: partial tile out (device-coherent
-        // stores), one counter per (column block, row tile); the last arrival
-        // sums each row's splits in split order (deterministic)
-        const int S = gridDim.z, proj = blockIdx.x & 1;
+    if (p.gu || p.handoff) {
+        // partial-tile hand-off (gate/up mode, or plain mode with k-splits):
+        // partial tile out (device-coherent stores), one counter per (column
+        // block, row tile); the last of the np x S arrivals sums each row's
+        // splits in split order (deterministic)
+        const int np = p.gu ? 2 : 1;
+        const int S = gridDim.z, proj = p.gu ? (int)(blockIdx.x & 1) : 0;
         const size_t rs = (size_t)p.M * 128;  // between splits
-        float* part = p.partials + ((size_t)(bx * 2 + proj) * S + sidx) * rs + (size_t)m0 * 128;
+        float* part = p.partials + ((size_t)(bx * np + proj) * S + sidx) * rs + (size_t)m0 * 128;
         for (int idx = tid; idx < rows * 128; idx += FAT_THREADS) coherent_store(part + idx, ct[idx]);
         wait_stores();
         __syncthreads();
@@ -287,11 +294,29 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
         int* ctr = p.counters + (size_t)bx * gridDim.y + blockIdx.y;
         if (tid == 0) {
             const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            gu_last = old == 2 * S - 1;
+            gu_last = old == np * S - 1;
         }
         __syncthreads();
         if (!gu_last) return;
         if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!p.gu) {
+            const float* pv = p.partials + (size_t)bx * S * rs + (size_t)m0 * 128 + 2 * lane;
+            const float sva = __low2float(svv), svb = __high2float(svv);
+            for (int row = cw; row < rows; row += FAT_THREADS / 64) {
+                const float* const src[1] = {pv + row * 128};
+                float2 v2[1];
+                sum_splits2<1, 4>(src, rs, S, v2);
+                float va = v2[0].x, vb = v2[0].y;
+                if constexpr (RAW) {
+                    const float sx = kMul1Bias * fat_row_sum(p.rowsum, p.k >> 7, m0 + row, 0, p.k >> 7, lane);
+                    va = va * kMul1Kinv + sx;
+                    vb = vb * kMul1Kinv + sx;
+                }
+                fwht128_pair_fast(va, vb, lane);
+                st_h2(gptr(p.out16) + (size_t)(m0 + row) * p.n + c0, h2_rn((va * kHadNorm) * sva, (vb * kHadNorm) * svb));
+            }
+            return;
+        }
         const float* pg = p.partials + (size_t)(bx * 2) * S * rs + (size_t)m0 * 128 + 2 * lane;
         const float* pu = p.partials + (size_t)(bx * 2 + 1) * S * rs + (size_t)m0 * 128 + 2 * lane;
         const __half2 svg = ld_h2(gptr(p.svh) + c0), svu = ld_h2(gptr(p.svh2) + c0);
