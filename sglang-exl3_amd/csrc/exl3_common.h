@@ -60,12 +60,12 @@ inline int env_int(const char* name, int dflt) {
     return atoi(v);
 }
 
-// exl3_gemm: GEMV kernels up to this many rows, the MFMA GEMM above
-// (gemm_gemv_rows(), env override).  Config 2 (K = 4, MCG), graph-timed,
-// GEMV / MFMA: m = 4 / 8 / 10 / 12 / 14 / 15: 14.6 / 18.7 / 20.8 / 22.7 / 24.4 /
-// 25.7 us against 20.1 / 21.2 / 22.0 / 22.2 / 23.2 / 23.2 us.
-constexpr int kGemmGemvRows = 11;
-int gemm_gemv_rows();
+// exl3_gemm: GEMV kernels up to this many rows for outputs narrower than
+// 12288 columns, kGemmGemvRowsWide from 12288 and one row fewer from 24576;
+// the MFMA GEMM above (gemm_gemv_rows(n), env override).
+constexpr int kGemmGemvRows = 12;
+constexpr int kGemmGemvRowsWide = 8;
+int gemm_gemv_rows(int n);
 
 }  // namespace exl3
 

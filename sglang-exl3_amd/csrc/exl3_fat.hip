@@ -61,6 +61,15 @@ struct FatPlan {
 // 222.6 / 129.6, 768: 227.9 / 330.7 / 131.4.  128-row narrow tiles never win
 // (kept as the EXL3_FAT_MT=128 override).
 constexpr int kFatNarrowMaxRows = 256;
+// ... and only when they make at least this many tiles: a smaller wide grid
+// needs fp32-atomic k-splits, and the narrow kernel with its split hand-off
+// is faster there.  Graph-timed, wide / narrow: k = 14336, n = 4096, M = 320 /
+// 512 / 768 / 1024 / 1536 / 2048 (20 / 32 / 48 / 64 / 96 / 128 tiles): 153.0 /
+// 171.0 / 258.1 / 273.4 / 240.0 / 269.6 us against 101.4 / 129.9 / 191.9 /
+// 241.3 / 361.0 / 458.5; k = 4096, n = 7168, M = 768 / 1024 (84 / 112 tiles):
+// 151.0 / 99.0 against 105.6 / 131.1; n = 14336, M = 320 (112 tiles): 91.7
+// against 97.0.
+constexpr int kFatWideMinTiles = 96;
 
 // k-splits of the narrow kernel: the most that keep the grid at or under
 // kFatNarrowWgs workgroups (about two per CU; more splits add partial sums
@@ -71,11 +80,26 @@ constexpr int kFatNarrowMaxRows = 256;
 // 45.4, M = 128: 80.1 / 123.1 / 161.3 / 234.5.  (Gate/up mode has its own rule,
 // plan_gate_up_fat.)
 constexpr long long kFatNarrowWgs = 512;
+// With fp16 output the splits hand partial tiles to the last split
+// (fat_handoff), which costs less than the atomics: the most splits that keep
+// the grid at or under kFatHandoffWgs workgroups (about the resident count)
+// with at least kFatHandoffMinSteps steps per split.  Graph-timed, splits
+// 1 / 2 / 4 / 8 / 16 with the hand-off: k = 4096, n = 14336, K = 4: M = 16:
+// 37.3 / 24.6 / 20.6 / 22.8 / 26.5 us, 64: 67.3 / 47.9 / 37.9 / 43.9 / 62.6,
+// 128: 68.4 / 54.8 / 51.9 / 59.4 / 80.5, 192: 78.0 / 65.9 / 69.2 / 79.2 /
+// 102.7, 256: 80.8 / 79.4 / 78.2 / 92.2 / 120.9; n = 28672, K = 3: M = 64:
+// 69.4 / 52.8 / 50.1 / 58.5 / 77.5, 128: 81.6 / 77.4 / 77.1 / 90.8 / 118.6;
+// k = 14336, n = 4096, K = 3: M = 192: 230.9 / 128.8 / 84.9 / 68.7 / 68.0.
+constexpr long long kFatHandoffWgs = 1024;
+constexpr int kFatHandoffMinSteps = 16;
 
-bool fat_wide_allowed() {
-    const char* env = getenv("EXL3_FAT_WIDE");
-    return !(env && env[0] == '0');
-}
+bool fat_handoff_on() { return env_int("EXL3_FAT_HANDOFF", 1) != 0; }
+
+// EXL3_FAT_WIDE: 0 never wide tiles, 2 wide tiles whenever the shape allows
+// them (M > kFatNarrowMaxRows, n a multiple of 256; tests of the wide
+// kernel), otherwise the measured rule.
+int fat_wide_mode() { return env_int("EXL3_FAT_WIDE", 1); }
+bool fat_wide_allowed() { return fat_wide_mode() != 0; }
 
 // Compute units of the current device (one wide-tile workgroup each), cached
 // per device.
@@ -113,11 +137,14 @@ int wide_tail_tiles(int m, int k, int n, bool gu) {
     return fat_tail_tiles(tiles, k / 64);
 }
 
-FatPlan plan_fat(int M, int k, int n) {
+// f16out: a call with fp16 output (exl3_gemm), whose narrow k-splits use the
+// partial-tile hand-off (fat_handoff) unless EXL3_FAT_HANDOFF=0.
+FatPlan plan_fat(int M, int k, int n, bool f16out) {
     FatPlan pl;
     const int ksteps = k / 64;
     pl.splits = 1;
-    if (fat_wide_allowed() && M > kFatNarrowMaxRows && n % FB_COLS == 0) {
+    if (fat_wide_allowed() && M > kFatNarrowMaxRows && n % FB_COLS == 0 &&
+        (fat_wide_mode() == 2 || (long long)(n / FB_COLS) * ((M + FB_ROWS - 1) / FB_ROWS) >= kFatWideMinTiles)) {
         pl.mt = FAT_MT_WIDE;
         const long long base = (long long)(n / FB_COLS) * ((M + FB_ROWS - 1) / FB_ROWS);
         while (base * pl.splits < 96 && pl.splits < 16 && ksteps % (4 * pl.splits) == 0) pl.splits *= 2;
@@ -127,9 +154,12 @@ FatPlan plan_fat(int M, int k, int n) {
     const int fmt = env_int("EXL3_FAT_MT", 0);  // tuning override: 16, 64 or 128 rows per tile
     if (fmt == 16 || fmt == 64 || fmt == 128) pl.mt = fmt;
     const long long base = (long long)(n / 128) * ((M + pl.mt - 1) / pl.mt);
+    const bool ho = f16out && fat_handoff_on();
+    const long long wgs = ho ? kFatHandoffWgs : kFatNarrowWgs;
+    const int min_steps = ho ? kFatHandoffMinSteps : 0;
     const int forced = env_int("EXL3_FAT_SPLITS", 0);  // tuning override (power of two)
-    while ((forced ? pl.splits < forced : base * pl.splits * 2 <= kFatNarrowWgs) && pl.splits < 16 &&
-           ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
+    while ((forced ? pl.splits < forced : base * pl.splits * 2 <= wgs && ksteps / (2 * pl.splits) >= min_steps) &&
+           pl.splits < 16 && ksteps % (2 * pl.splits) == 0 && (ksteps / (2 * pl.splits)) % FAT_CH == 0)
         pl.splits *= 2;
     return pl;
 }
@@ -161,8 +191,7 @@ bool fat_raw(int cb, int mt) { return cb == 2 && mt == 16 && env_int("EXL3_FAT_R
 // keeps the atomic path (ablation).
 bool fat_handoff(const FatPlan& pl, int m, int n) {
     return pl.splits > 1 && pl.mt != FAT_MT_WIDE &&
-           (size_t)(n / 128) * (size_t)((m + pl.mt - 1) / pl.mt) <= kWsMaxCounters &&
-           env_int("EXL3_FAT_HANDOFF", 1) != 0;
+           (size_t)(n / 128) * (size_t)((m + pl.mt - 1) / pl.mt) <= kWsMaxCounters && fat_handoff_on();
 }
 
 // tail: tail-split tiles (unsplit wide launch with fp16 output; 0 = none),
@@ -174,7 +203,7 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
             const int64_t* token_idx, const uint16_t* route_w, int M, int k, int n, int K, int cb, bool zero_first,
             hipStream_t st, int tail = 0, char* tail_part = nullptr, int* tail_sync = nullptr,
             const float* rowsum = nullptr, float* partials = nullptr, int* counters = nullptr) {
-    const FatPlan pl = plan_fat(M, k, n);
+    const FatPlan pl = plan_fat(M, k, n, out16 != nullptr);
     FatParams p{};
     if (partials && pl.splits > 1) {
         p.handoff = 1;
@@ -218,7 +247,7 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
 
 }  // namespace
 
-// Prefill path of exl3_gemm (m > gemm_gemv_rows()).  Scratch after the workspace's zeroed
+// Prefill path of exl3_gemm (m > gemm_gemv_rows(n)).  Scratch after the workspace's zeroed
 // regions (shared with the GEMV kernels, which need them to stay zero); an
 // unsplit GEMM stores fp16 straight to y.
 // xr: the rotated rows (fp16 m*k), then their chunk sums (fp32 m*k/128).
@@ -228,7 +257,7 @@ size_t fat_xr_bytes(int m, int k) { return fat_xr_only_bytes(m, k) + (((size_t)m
 // hand-off) | out fp32 m*n (wide plan with k-splits) | tail-split hand-off
 // tiles (unsplit wide launch)].
 size_t fat_gemm_scratch_bytes(int m, int k, int n) {
-    const FatPlan pl = plan_fat(m, k, n);
+    const FatPlan pl = plan_fat(m, k, n, true);
     const bool split = pl.splits > 1;
     const size_t tail = (!split && pl.mt == FAT_MT_WIDE) ? fat_tail_bytes(wide_tail_tiles(m, k, n, false)) : 0;
     const size_t out = fat_handoff(pl, m, n) ? (size_t)pl.splits * m * n * 4 : (size_t)m * n * 4;
@@ -244,7 +273,7 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
     EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4), "exl3_gemm: misaligned pointer");
     __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsScratchOffset);
     float* o32 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsScratchOffset + fat_xr_bytes(m, k));
-    const FatPlan pl = plan_fat(m, k, n);
+    const FatPlan pl = plan_fat(m, k, n, true);
     float* rs = fat_raw(cb, pl.mt)
                     ? reinterpret_cast<float*>(reinterpret_cast<char*>(xr) + fat_xr_only_bytes(m, k))
                     : nullptr;
@@ -396,6 +425,6 @@ extern "C" int exl3_fat_gemm_scatter(const uint16_t* a, const int16_t* trellis, 
 
 extern "C" size_t exl3_gemm_workspace_size(int m, int k, int n, int K) {
     if (m < 1 || k < 128 || n < 128) return 0;
-    if (m <= gemm_gemv_rows()) return exl3_gemv_workspace_size(m, k, n, K, 1);
+    if (m <= gemm_gemv_rows(n)) return exl3_gemv_workspace_size(m, k, n, K, 1);
     return fat_gemm_scratch_bytes(m, k, n);
 }

@@ -61,12 +61,17 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
 
 // Rows up to which exl3_gemm runs the GEMV kernels; above, the input is
 // rotated once and the MFMA GEMM runs (env EXL3_GEMM_GEMV_ROWS, at most 64).
-// Graph-timed on config 2 (k=4096, n=14336, K=4), GEMV kernels against the
-// MFMA path: m = 8: 19.3 / 25.9 us, 12: 22.9 / 26.3, 16: 30.7 / 29.3,
-// 32: 58.1 / 33.9, 64: 116.9 / 53.0.
-int gemm_gemv_rows() {
+// The MFMA path parallelises over 128-column blocks, so it wins earlier on
+// wide outputs.  Graph-timed, GEMV / MFMA (split hand-off), K = 3 unless
+// noted: k = 4096, n = 7168: m = 8 / 12 / 16: 13.6 / 16.2 / 18.4 against 15.7 /
+// 16.7 / 17.3 us; k = 14336, n = 4096: m = 8 / 12 / 16: 18.8 / 24.1 / 32.6
+// against 23.9 / 25.2 / 26.8; k = 4096, n = 14336, K = 4: m = 8 / 9 / 12: 18.7 /
+// 20.0 / 22.9 against 18.7 / 19.5 / 19.9; k = 4096, n = 28672: m = 4 / 8: 23.7
+// / 30.9 against 27.6 / 28.3.
+int gemm_gemv_rows(int n) {
     const char* v = getenv("EXL3_GEMM_GEMV_ROWS");
-    const int r = (v && *v) ? atoi(v) : kGemmGemvRows;
+    const int r = (v && *v) ? atoi(v) : (n >= 24576 ? kGemmGemvRowsWide - 1
+                                                    : (n >= 12288 ? kGemmGemvRowsWide : kGemmGemvRows));
     return r < 0 ? 0 : (r > 64 ? 64 : r);
 }
 
@@ -427,7 +432,7 @@ extern "C" int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16
     EXL3_REQUIRE(aligned(x, 4) && aligned(y, 4) && aligned(suh, 4) && aligned(svh, 4) && aligned(trellis, 16),
                  "exl3_gemm: misaligned pointer");
     hipStream_t st = as_stream(stream);
-    if (m > gemm_gemv_rows()) return fat_gemm_rows(x, trellis, suh, svh, y, m, k, n, K, codebook, workspace,
+    if (m > gemm_gemv_rows(n)) return fat_gemm_rows(x, trellis, suh, svh, y, m, k, n, K, codebook, workspace,
                                                workspace_bytes, st);
     for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
         const int mc = (m - r0) < kMaxGemvRows ? (m - r0) : kMaxGemvRows;

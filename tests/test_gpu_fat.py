@@ -86,14 +86,16 @@ def test_fat_wide_tiles_every_width(K, cb):
     print(f"case: fat wide M={M} k={k} n={n} K={K} cb={cb}", flush=True)
     tr, su, sv = make_weight(k, n, K, seed=100 + 3 * K + cb)
     a = _rotate(make_x(M, k, seed=K + 10 * cb), su)
-    check_close(_fat(a, tr, sv, K, cb, M, n), _ref(a, tr, sv, K, cb), f"fat wide K={K} cb={cb}")
+    out = _with_env("EXL3_FAT_WIDE", "2", lambda: _fat(a, tr, sv, K, cb, M, n))
+    check_close(out, _ref(a, tr, sv, K, cb), f"fat wide K={K} cb={cb}")
 
 
 @pytest.mark.parametrize("M,k,n,K,cb", [(512, 1024, 512, 3, 2), (257, 512, 768, 4, 1), (65, 2048, 256, 2, 0),
                                         (1100, 128, 512, 5, 1)])
-@pytest.mark.parametrize("wide", ["1", "0"])
+@pytest.mark.parametrize("wide", ["2", "1", "0"])
 def test_fat_wide_and_narrow_kernels(M, k, n, K, cb, wide):
-    """The same shapes through the wide-tile kernel and the narrow one (EXL3_FAT_WIDE=0)."""
+    """The same shapes through the wide-tile kernel (EXL3_FAT_WIDE=2), the
+    default plan and the narrow kernel (EXL3_FAT_WIDE=0)."""
     print(f"case: fat M={M} k={k} n={n} K={K} cb={cb} wide={wide}", flush=True)
     tr, su, sv = make_weight(k, n, K, seed=M + n)
     a = _rotate(make_x(M, k, seed=M + 1), su)
@@ -101,7 +103,8 @@ def test_fat_wide_and_narrow_kernels(M, k, n, K, cb, wide):
     check_close(out, _ref(a, tr, sv, K, cb), f"fat M={M} wide={wide}")
 
 
-def test_fat_wide_scatter_accumulates():
+def test_fat_wide_scatter_accumulates(monkeypatch):
+    monkeypatch.setenv("EXL3_FAT_WIDE", "2")  # the wide-tile kernel at this small grid
     M, k, n, K = 300, 512, 512, 3
     tr, su, sv = make_weight(k, n, K, seed=15)
     a = _rotate(make_x(M, k, seed=16), su)
@@ -211,9 +214,12 @@ def test_mul1_raw_entries(op, m, monkeypatch):
     (row sum of the rotated x over the split's k range).  k = 14336 (112 chunk
     sums per row), 16-row tiles with k-splits (m = 16): against the oracle and
     close to the decoded path (EXL3_FAT_RAW=0).  The 64-row tiles (m = 48) and
-    the wide tiles (gemm m = 300: 16 fp32-atomic k-splits; gate/up m = 200:
-    tail-split k-halves) decode values and are checked at the same k."""
+    the wide tiles (gemm m = 300, forced by EXL3_FAT_WIDE=2: 16 fp32-atomic
+    k-splits; gate/up m = 200: tail-split k-halves) decode values and are
+    checked at the same k."""
     k, n, K, cb = 14336, 256, 3, 2
+    if op == "gemm" and m > 256:
+        monkeypatch.setenv("EXL3_FAT_WIDE", "2")
     print(f"case: raw mul1 {op} m={m} k={k} n={n}", flush=True)
     x = torch.from_numpy(make_x(m, k, seed=51 + m)).cuda()
     if op == "gemm":

@@ -110,10 +110,13 @@ def test_gemv_zero_trellis_closed_form():
         assert np.abs(y[:, mask]).max() <= 1e-3 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("m", [1, 11, 12, 16, 64, 130])
-def test_gemm_any_rows(m):
-    print(f"case: gemm m={m}", flush=True)
-    k, n, K = 512, 256, 3
+@pytest.mark.parametrize("m,n", [(1, 256), (12, 256), (13, 256), (16, 256), (64, 256), (130, 256), (8, 12288),
+                                 (9, 12288)])
+def test_gemm_any_rows(m, n):
+    """exl3_gemm on both sides of its GEMV / MFMA crossover (12 rows below
+    12288 output columns, 8 from there)."""
+    print(f"case: gemm m={m} n={n}", flush=True)
+    k, K = 512, 3
     trellis, suh, svh = make_weight(k, n, K, seed=40 + m)
     x = make_x(m, k, seed=41 + m)
     xd, tr, su, sv = to_dev(x, trellis, suh, svh)
