@@ -393,12 +393,13 @@ __device__ __forceinline__ uint32_t mul1_raw_pair(uint32_t s0, uint32_t s1) {
 
 // Exact-rounding decode (dequant / decode ops): fp16 bits of two values.
 // RAW (mul1, round to nearest): the raw entries of mul1_raw_pair instead.
+// Windows come from buf and the middle words mid (window_mid).
 template <int K, int CB, bool RZ, int H, int C, int P, bool RAW = false>
-__device__ __forceinline__ uint32_t frag_pair(const uint32_t* buf) {
+__device__ __forceinline__ uint32_t frag_pair(const uint32_t* buf, const uint32_t* mid) {
     constexpr int e0 = 2 * P, e1 = 2 * P + 1;
     constexpr int u0 = 16 * H + (e0 & 3) + 8 * (e0 >> 2) + 4 * C;
     constexpr int u1 = 16 * H + (e1 & 3) + 8 * (e1 >> 2) + 4 * C;
-    uint32_t s0 = window<K, u0>(buf), s1 = window<K, u1>(buf);
+    uint32_t s0 = window_mid<K, u0>(buf, mid), s1 = window_mid<K, u1>(buf, mid);
     if constexpr (RAW) {
         static_assert(CB == 2 && !RZ, "raw entries: mul1, matmul side");
         return mul1_raw_pair(s0, s1);
@@ -410,21 +411,27 @@ __device__ __forceinline__ uint32_t frag_pair(const uint32_t* buf) {
 }
 
 template <int K, int CB, bool RZ, int H, int C, bool RAW = false>
-__device__ __forceinline__ void frag_decode(const uint32_t* buf, uint32_t* f) {
-    f[0] = frag_pair<K, CB, RZ, H, C, 0, RAW>(buf);
-    f[1] = frag_pair<K, CB, RZ, H, C, 1, RAW>(buf);
-    f[2] = frag_pair<K, CB, RZ, H, C, 2, RAW>(buf);
-    f[3] = frag_pair<K, CB, RZ, H, C, 3, RAW>(buf);
+__device__ __forceinline__ void frag_decode(const uint32_t* buf, const uint32_t* mid, uint32_t* f) {
+    f[0] = frag_pair<K, CB, RZ, H, C, 0, RAW>(buf, mid);
+    f[1] = frag_pair<K, CB, RZ, H, C, 1, RAW>(buf, mid);
+    f[2] = frag_pair<K, CB, RZ, H, C, 2, RAW>(buf, mid);
+    f[3] = frag_pair<K, CB, RZ, H, C, 3, RAW>(buf, mid);
 }
 
 // Decode the 32 values of one lane's group into fp16 words frag[c][h][p]
-// (values 2p, 2p+1 of column q + 8c, run h; tile row 4h + kofs(e)).
+// (values 2p, 2p+1 of column q + 8c, run h; tile row 4h + kofs(e)).  The
+// straddling windows are cut from one middle word per word boundary (a
+// single v_bfe each instead of v_alignbit + mask: config 3 gate/up M = 16 /
+// 128 30.3 / 81.6 -> 29.6 / 79.5 us, MoE prefill 2048 tokens 528.6 -> 515.7).
 template <int K, int CB, bool RZ, bool RAW = false>
 __device__ __forceinline__ void decode_group(const uint32_t* buf, uint32_t frag[2][2][4]) {
-    frag_decode<K, CB, RZ, 0, 0, RAW>(buf, frag[0][0]);
-    frag_decode<K, CB, RZ, 1, 0, RAW>(buf, frag[0][1]);
-    frag_decode<K, CB, RZ, 0, 1, RAW>(buf, frag[1][0]);
-    frag_decode<K, CB, RZ, 1, 1, RAW>(buf, frag[1][1]);
+    uint32_t mid[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) mid[j] = __builtin_amdgcn_alignbit(buf[j], buf[j + 1], 16);
+    frag_decode<K, CB, RZ, 0, 0, RAW>(buf, mid, frag[0][0]);
+    frag_decode<K, CB, RZ, 1, 0, RAW>(buf, mid, frag[0][1]);
+    frag_decode<K, CB, RZ, 0, 1, RAW>(buf, mid, frag[1][0]);
+    frag_decode<K, CB, RZ, 1, 1, RAW>(buf, mid, frag[1][1]);
 }
 
 }  // namespace exl3
