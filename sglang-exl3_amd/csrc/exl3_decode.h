@@ -360,24 +360,11 @@ __device__ __forceinline__ uint32_t decode_pair_word(uint32_t s) {
     else return cb_mask(x);
 }
 
-template <int K, int CB, int U>
-__device__ __forceinline__ void pair_one(const uint32_t* buf, uint32_t* out) {
-    out[U] = decode_pair_word<CB>(window<K, U>(buf));
-}
-
-template <int K, int CB, int... Us>
-__device__ __forceinline__ void pair_all(const uint32_t* buf, uint32_t* out, std::integer_sequence<int, Us...>) {
-    (pair_one<K, CB, Us>(buf, out), ...);
-}
-
-// All 32 values of a lane's group in pair form, in value order u = 0..31.
-// Writing u = 8Q + 4c + t (Q = 0..3, c = 0..1, t = 0..3): value u is column
-// q + 8c of the tile at row k = 4(Q >> 1) + kofs(4(Q & 1) + t), so each run
-// of four consecutive values is one MFMA B fragment (one column, 4 rows).
-template <int K, int CB>
-__device__ __forceinline__ void decode_group_pairs(const uint32_t* buf, uint32_t out[32]) {
-    pair_all<K, CB>(buf, out, std::make_integer_sequence<int, 32>{});
-}
+// Pair-form value order of a lane's group (the GEMV and MoE kernels decode
+// u = 4F .. 4F + 3 per MFMA fragment F): writing u = 8Q + 4c + t (Q = 0..3,
+// c = 0..1, t = 0..3), value u is column q + 8c of the tile at row
+// k = 4(Q >> 1) + kofs(4(Q & 1) + t), so each run of four consecutive values
+// is one MFMA B fragment (one column, 4 rows).
 
 // Tile row of value slot t (0..3) of quarter Q (0..3).
 __host__ __device__ constexpr int quarter_row(int Q, int t) { return 4 * (Q >> 1) + kofs(4 * (Q & 1) + t); }
