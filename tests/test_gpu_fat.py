@@ -244,3 +244,27 @@ def test_mul1_raw_entries(op, m, monkeypatch):
     dec = run()
     torch.cuda.synchronize()
     check_close(raw.float().cpu().numpy(), dec.float().cpu().numpy(), f"raw vs decoded {op} m={m}")
+
+
+@pytest.mark.parametrize("m,cb", [(16, 1), (64, 2)])
+def test_gemm_split_handoff_repeatable(m, cb, monkeypatch):
+    """exl3_gemm's narrow k-splits hand partial tiles to the last split of each
+    (column block, row tile): against the oracle, bit-identical over repeated
+    calls (the counters reset themselves), and close to the fp32-atomic path
+    (EXL3_FAT_HANDOFF=0).  k = 4096, n = 2048: four splits of 16 steps."""
+    k, n, K = 4096, 2048, 3
+    print(f"case: gemm split hand-off m={m} cb={cb}", flush=True)
+    x = torch.from_numpy(make_x(m, k, seed=61 + m)).cuda()
+    tr, su, sv = make_weight(k, n, K, seed=62)
+    d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
+    run = lambda: torch.ops.sglang_exl3.exl3_gemm(x, *d, K, cb == 1)
+    outs = [run() for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0]), "split hand-off: repeated calls differ"
+    ref = oracle.matmul(x.cpu().numpy(), oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    check_close(outs[0].float().cpu().numpy(), ref, f"split hand-off m={m}")
+    monkeypatch.setenv("EXL3_FAT_HANDOFF", "0")
+    atomic = run()
+    torch.cuda.synchronize()
+    check_close(outs[0].float().cpu().numpy(), atomic.float().cpu().numpy(), f"hand-off vs atomics m={m}")
