@@ -118,18 +118,23 @@ int exl3_gemv(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, co
 int exl3_gemv_noalloc(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
                       uint16_t* y, int m, int k, int n, int K, int codebook, void* stream);
 
-/* Same product for any number of rows m >= 1: up to 64 rows the GEMV kernel;
+/* Same product for any number of rows m >= 1: the GEMV kernels up to 12 rows
+ * (8 from n = 12288 output columns, 7 from 24576; env EXL3_GEMM_GEMV_ROWS);
  * above, the input is rotated once and the MFMA GEMM (exl3_fat_gemm's
- * kernel) runs over it (workspace: exl3_gemm_workspace_size).
+ * kernels) runs over it with fp16 output, its k-splits handing partial tiles
+ * to the last split (workspace: exl3_gemm_workspace_size).  Deterministic.
  * Replaces exl3_gemm (csrc/bindings.cpp:110-115 -> csrc/exl3_gemm.cu:9-31;
  * torch op sglang_exl3::exl3_gemm, src/sglang_exl3/ops.py:77-93). */
 int exl3_gemm(const uint16_t* x, const int16_t* trellis, const uint16_t* suh, const uint16_t* svh,
               uint16_t* y, int m, int k, int n, int K, int codebook, void* workspace,
               size_t workspace_bytes, void* stream);
 
-/* Scratch bytes exl3_gemm needs for m rows: the GEMV workspace for m <= 64,
- * above that the prefill scratch (rotated input m*k fp16 + m*n fp32).  The
- * workspace must start zero-filled (counters), as for exl3_gemv. */
+/* Scratch bytes exl3_gemm needs for m rows: the GEMV workspace where the
+ * GEMV kernels run, above that the prefill scratch (rotated input m*k fp16
+ * and its per-128 row sums, then the k-splits' fp32 partial tiles or the
+ * wide kernel's tail hand-off).  It depends on the current device's CU
+ * count.  The workspace must start zero-filled (counters), as for exl3_gemv;
+ * every call leaves the counters zero. */
 size_t exl3_gemm_workspace_size(int m, int k, int n, int K);
 
 /* Many-row EXL3 GEMM on MFMA with the input already rotated:
