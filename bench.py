@@ -404,7 +404,9 @@ def profile_pass(torch, L, kind, steps):
     known byte count (the calibration kernel whose FETCH_SIZE / WRITE_SIZE
     readings scale the counters).
       gemv: `steps` m=1 config-2 GEMVs over the rotating copies (copy: one packed weight);
-      moe:  `steps` config-4 layer calls at B=16 over 8 layer copies (copy: 16 experts' packs)."""
+      moe:  `steps` config-4 layer calls at B=16 over 8 layer copies (copy: 16 experts' packs);
+      gate_up: `steps` config-3 exl3_gate_up_swiglu calls at M=16 over the 8 pack copies (copy: one
+            gate+up pair's packed bytes)."""
     if kind == "gemv":
         weights = gemv_weights(torch)
         k, n, K = K_DIM, N_DIM, BITS
@@ -420,6 +422,20 @@ def profile_pass(torch, L, kind, steps):
                 raise RuntimeError(L.exl3_last_error().decode())
         nbytes = k * n * K // 8
         ncopy = NCOPY
+    elif kind == "gate_up":
+        g = torch.Generator(device="cuda")
+        g.manual_seed(31)
+        shape = (GU_K // 16, GU_N // 16, 16 * GU_BITS)
+        packs = [(_rand_trellis(torch, shape, g), _rand_trellis(torch, shape, g)) for _ in range(GU_COPIES)]
+        suh = _sign_f16(torch, GU_K, g)
+        svg = _sign_f16(torch, GU_N, g, 4.0 / GU_K ** 0.5)
+        svu = _sign_f16(torch, GU_N, g, 4.0 / GU_K ** 0.5)
+        x = torch.randn(16, GU_K, dtype=torch.float16, device="cuda", generator=g)
+        for c in range(steps):
+            tg, tu = packs[c % GU_COPIES]
+            torch.ops.sglang_exl3.exl3_gate_up_swiglu(x, suh, tg, svg, tu, svu, GU_BITS, 2, 0.0)
+        nbytes = 2 * GU_K * GU_N * GU_BITS // 8
+        ncopy = GU_COPIES
     else:
         layers = [MoeWeights(torch, 1000 + i) for i in range(8)]
         B = 16
@@ -512,7 +528,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the batched-MoE layer leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the config-3 and config-5 legs")
-    ap.add_argument("--profile-pass", choices=("gemv", "moe"),
+    ap.add_argument("--profile-pass", choices=("gemv", "moe", "gate_up"),
                     help="eager launches plus a copy-kernel calibration, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
