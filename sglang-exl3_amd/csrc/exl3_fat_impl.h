@@ -36,6 +36,12 @@ namespace exl3 {
 constexpr int FAT_THREADS = 256;  // 4 waves x 32 output columns
 constexpr int FAT_CH = 4;         // steps per staged A chunk (256 k)
 constexpr int FAT_ROWB = FAT_CH * 4 * 2 * 16 + 16;  // bytes per staged A row (+16: bank spread)
+// 16-row tiles stage 8 steps per chunk (16.6 KB of LDS, half the barriers;
+// their ~75 VGPRs bound the occupancy first): config 3 gate/up M = 16 29.3 ->
+// 28.6 us, exl3_gemm n = 28672 M = 16 30.2 -> 29.4.  A partial last chunk is
+// fine: its missing slices stage zeros and its steps are skipped.
+template <int MT> __host__ __device__ constexpr int fat_ch() { return MT == 16 ? 8 : FAT_CH; }
+template <int MT> __host__ __device__ constexpr int fat_rowb() { return fat_ch<MT>() * 4 * 2 * 16 + 16; }
 
 // A run of rows of one expert in compact (expert-sorted) order: one row tile
 // of the grouped mode, written by the MoE prefill routing kernel.
@@ -121,7 +127,7 @@ __host__ __device__ constexpr int fat_depth() {
 }
 
 inline size_t fat_smem_bytes(int mt) {
-    const size_t a = (size_t)mt * FAT_ROWB;
+    const size_t a = (size_t)mt * (mt == 16 ? fat_rowb<16>() : FAT_ROWB);
     const size_t c = (size_t)mt * 128 * sizeof(float);
     return a > c ? a : c;
 }
@@ -133,7 +139,8 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
     static_assert(!RAW || CB == 2, "raw entries: mul1");
     constexpr int RB = MT / 16;
     constexpr int D = fat_depth<K>();
-    static_assert(FAT_CH % D == 0, "the register slot of a step must be static inside a chunk");
+    constexpr int CH = fat_ch<MT>(), ROWB = fat_rowb<MT>();
+    static_assert(CH % D == 0, "the register slot of a step must be static inside a chunk");
     extern __shared__ __align__(16) unsigned char fat_smem[];
 
     const int sidx = blockIdx.z;
@@ -179,11 +186,11 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
         if (d < nsteps) load_words<K>(tb + (size_t)d * step_stride, w[d]);
 
     const EXL3_GLOBAL __half* ag = gptr(p.a);
-    for (int c0 = 0; c0 < nsteps; c0 += FAT_CH) {
-        // stage the chunk's A: rows x (FAT_CH * 4) slices of 16 k, permuted
+    for (int c0 = 0; c0 < nsteps; c0 += CH) {
+        // stage the chunk's A: rows x (CH * 4) slices of 16 k, permuted
         if (c0) __syncthreads();  // every wave is done with the previous chunk
-        for (int u = tid; u < MT * FAT_CH * 4; u += FAT_THREADS) {
-            const int row = u / (FAT_CH * 4), sl = u - row * (FAT_CH * 4);
+        for (int u = tid; u < MT * CH * 4; u += FAT_THREADS) {
+            const int row = u / (CH * 4), sl = u - row * (CH * 4);
             u32x4_t lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
             if (row < rows && c0 * 4 + sl < nsteps * 4) {
                 const EXL3_GLOBAL u32x4_t* src = reinterpret_cast<const EXL3_GLOBAL u32x4_t*>(
@@ -191,14 +198,14 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
                 lo = src[0];
                 hi = src[1];
             }
-            u32x4_t* dst = reinterpret_cast<u32x4_t*>(fat_smem + (size_t)row * FAT_ROWB + sl * 32);
+            u32x4_t* dst = reinterpret_cast<u32x4_t*>(fat_smem + (size_t)row * ROWB + sl * 32);
             dst[0] = u32x4_t{lo.x, hi.x, lo.y, hi.y};  // k pairs (0,1) (8,9) (2,3) (10,11)
             dst[1] = u32x4_t{lo.z, hi.z, lo.w, hi.w};  // k pairs (4,5) (12,13) (6,7) (14,15)
         }
         __syncthreads();
 
 #pragma unroll
-        for (int s = 0; s < FAT_CH; ++s) {
+        for (int s = 0; s < CH; ++s) {
             const int step = c0 + s;
             if (step >= nsteps) break;
             const int d = step % D;
@@ -209,13 +216,13 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
             uint32_t frag[2][2][4];
             decode_group<K, CB, false, RAW>(buf, frag);
             if (step + D < nsteps) load_words<K>(tb + (size_t)(step + D) * step_stride, w[d]);
-            const unsigned char* arow = fat_smem + (size_t)i * FAT_ROWB + (s * 4 + g) * 32;
+            const unsigned char* arow = fat_smem + (size_t)i * ROWB + (s * 4 + g) * 32;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 if (rb * 16 >= rows) break;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const half8_t A = *reinterpret_cast<const half8_t*>(arow + (size_t)rb * 16 * FAT_ROWB + h * 16);
+                    const half8_t A = *reinterpret_cast<const half8_t*>(arow + (size_t)rb * 16 * ROWB + h * 16);
 #pragma unroll
                     for (int c = 0; c < 2; ++c) {
                         const half8_t B = *reinterpret_cast<const half8_t*>(frag[c][h]);
