@@ -406,7 +406,8 @@ def profile_pass(torch, L, kind, steps):
       gemv: `steps` m=1 config-2 GEMVs over the rotating copies (copy: one packed weight);
       moe:  `steps` config-4 layer calls at B=16 over 8 layer copies (copy: 16 experts' packs);
       gate_up: `steps` config-3 exl3_gate_up_swiglu calls at M=16 over the 8 pack copies (copy: one
-            gate+up pair's packed bytes)."""
+            gate+up pair's packed bytes);
+      gate_up_prefill: the same at M=2048 (`steps` // 4 calls and copies)."""
     if kind == "gemv":
         weights = gemv_weights(torch)
         k, n, K = K_DIM, N_DIM, BITS
@@ -422,7 +423,7 @@ def profile_pass(torch, L, kind, steps):
                 raise RuntimeError(L.exl3_last_error().decode())
         nbytes = k * n * K // 8
         ncopy = NCOPY
-    elif kind == "gate_up":
+    elif kind in ("gate_up", "gate_up_prefill"):
         g = torch.Generator(device="cuda")
         g.manual_seed(31)
         shape = (GU_K // 16, GU_N // 16, 16 * GU_BITS)
@@ -430,7 +431,10 @@ def profile_pass(torch, L, kind, steps):
         suh = _sign_f16(torch, GU_K, g)
         svg = _sign_f16(torch, GU_N, g, 4.0 / GU_K ** 0.5)
         svu = _sign_f16(torch, GU_N, g, 4.0 / GU_K ** 0.5)
-        x = torch.randn(16, GU_K, dtype=torch.float16, device="cuda", generator=g)
+        M = 2048 if kind == "gate_up_prefill" else 16
+        if M > 16:
+            steps = max(1, steps // 4)
+        x = torch.randn(M, GU_K, dtype=torch.float16, device="cuda", generator=g)
         for c in range(steps):
             tg, tu = packs[c % GU_COPIES]
             torch.ops.sglang_exl3.exl3_gate_up_swiglu(x, suh, tg, svg, tu, svu, GU_BITS, 2, 0.0)
@@ -528,7 +532,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the batched-MoE layer leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the config-3 and config-5 legs")
-    ap.add_argument("--profile-pass", choices=("gemv", "moe", "gate_up"),
+    ap.add_argument("--profile-pass", choices=("gemv", "moe", "gate_up", "gate_up_prefill"),
                     help="eager launches plus a copy-kernel calibration, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
