@@ -268,3 +268,32 @@ def test_gemm_split_handoff_repeatable(m, cb, monkeypatch):
     atomic = run()
     torch.cuda.synchronize()
     check_close(outs[0].float().cpu().numpy(), atomic.float().cpu().numpy(), f"hand-off vs atomics m={m}")
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_fat_narrow_every_width(K, cb):
+    """Narrow kernel (64-row tiles, fp32 output through exl3_fat_gemm) at every
+    bit width and codebook: the decode's windows (middle words for the ones
+    that straddle two words) differ per K."""
+    M, k, n = 24, 512, 256
+    print(f"case: fat narrow M={M} k={k} n={n} K={K} cb={cb}", flush=True)
+    tr, su, sv = make_weight(k, n, K, seed=200 + 3 * K + cb)
+    a = _rotate(make_x(M, k, seed=K + 20 * cb), su)
+    check_close(_fat(a, tr, sv, K, cb, M, n), _ref(a, tr, sv, K, cb), f"fat narrow K={K} cb={cb}")
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [1, 2])
+def test_gemm_16_rows_every_width(K, cb):
+    """exl3_gemm at 16 rows (16-row tiles, k-split hand-off; mul1 reads raw
+    entries) at every bit width, against the oracle."""
+    m, k, n = 16, 1024, 256
+    print(f"case: gemm 16 rows K={K} cb={cb}", flush=True)
+    tr, su, sv = make_weight(k, n, K, seed=300 + 3 * K + cb)
+    x = make_x(m, k, seed=301 + K)
+    d = [torch.from_numpy(v).cuda() for v in (x, tr, su, sv)]
+    y = torch.ops.sglang_exl3.exl3_gemm(*d, K, cb == 1)
+    torch.cuda.synchronize()
+    ref = oracle.matmul(x, oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    check_close(y.float().cpu().numpy(), ref, f"gemm 16 rows K={K} cb={cb}")
