@@ -399,12 +399,13 @@ def big_moe_bench(torch):
 
 # ------------------------------------------------------------ profile passes
 
-def profile_pass(torch, L, kind, steps):
+def profile_pass(torch, L, kind, steps, moe_batch=16):
     """Eager launches for rocprofv3 counter runs, then `steps` device copies of a
     known byte count (the calibration kernel whose FETCH_SIZE / WRITE_SIZE
     readings scale the counters).
       gemv: `steps` m=1 config-2 GEMVs over the rotating copies (copy: one packed weight);
-      moe:  `steps` config-4 layer calls at B=16 over 8 layer copies (copy: 16 experts' packs);
+      moe:  `steps` config-4 layer calls at B = `moe_batch` (16 by default) over 8 layer copies
+            (copy: 16 experts' packs);
       gate_up: `steps` config-3 exl3_gate_up_swiglu calls at M=16 over the 8 pack copies (copy: one
             gate+up pair's packed bytes);
       gate_up_prefill: the same at M=2048 (`steps` // 4 calls and copies)."""
@@ -442,7 +443,7 @@ def profile_pass(torch, L, kind, steps):
         ncopy = GU_COPIES
     else:
         layers = [MoeWeights(torch, 1000 + i) for i in range(8)]
-        B = 16
+        B = moe_batch
         ids, w = moe_routing(B, seed=B * 1000)
         x = torch.from_numpy(np.random.default_rng(B + 5).standard_normal((B, MOE_H)).astype(np.float16)).cuda()
         idd, wd = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
@@ -534,6 +535,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the config-3 and config-5 legs")
     ap.add_argument("--profile-pass", choices=("gemv", "moe", "gate_up", "gate_up_prefill"),
                     help="eager launches plus a copy-kernel calibration, for rocprofv3 counter runs")
+    ap.add_argument("--moe-batch", type=int, default=16, choices=(1, 16, 64),
+                    help="tokens per layer call of --profile-pass moe")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported "
@@ -547,7 +550,7 @@ def main():
     L = _lib.lib()
     ops.register_custom_ops()
     if args.profile_pass:
-        profile_pass(torch, L, args.profile_pass, args.steps)
+        profile_pass(torch, L, args.profile_pass, args.steps, args.moe_batch)
         return
 
     weights = gemv_weights(torch)
