@@ -270,6 +270,26 @@ def test_gemm_split_handoff_repeatable(m, cb, monkeypatch):
     check_close(outs[0].float().cpu().numpy(), atomic.float().cpu().numpy(), f"hand-off vs atomics m={m}")
 
 
+@pytest.mark.parametrize("m", [13, 40, 100, 250])
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_gemm_split_handoff_ragged_rows(m, cb):
+    """The split hand-off on row counts that leave the last row tile partial
+    (16-row tiles at 13 rows, 64-row tiles above), every codebook (3INST
+    through exl3_linear): k = 2048 gives two splits of 16 steps, n = 384 three
+    column blocks.  Against the oracle, and bit-identical on a repeat call."""
+    k, n, K = 2048, 384, 4
+    print(f"case: gemm split hand-off ragged m={m} cb={cb}", flush=True)
+    x = torch.from_numpy(make_x(m, k, seed=71 + m)).cuda()
+    tr, su, sv = make_weight(k, n, K, seed=72 + cb)
+    d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
+    run = lambda: torch.ops.sglang_exl3.exl3_linear(x, *d, K, cb)
+    first, again = run(), run()
+    torch.cuda.synchronize()
+    assert torch.equal(first, again), "split hand-off: repeated calls differ"
+    ref = oracle.matmul(x.cpu().numpy(), oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    check_close(first.float().cpu().numpy(), ref, f"split hand-off ragged m={m} cb={cb}")
+
+
 @pytest.mark.parametrize("K", range(1, 9))
 @pytest.mark.parametrize("cb", [0, 1, 2])
 def test_fat_narrow_every_width(K, cb):
