@@ -1,9 +1,11 @@
 """GPU parity of the fused gate+up SwiGLU op (exl3_gate_up_swiglu) against the
 oracle: out = silu(min(x W_g, L)) * clamp(x W_u, -L, L), both weights sharing
 the input rotation suh, as the reference's fused gate/up path does
-(src/sglang_exl3/exl3.py:1184-1206).  Up to 64 rows the GEMV kernel (gate and
-up rounded to fp16 first), above the wide-tile MFMA kernel (fp32).  Bar:
-max-abs-err <= 2e-2 * rms(ref), cosine >= 0.9999."""
+(src/sglang_exl3/exl3.py:1184-1206).  Up to 3 rows the GEMV kernel (gate and
+up rounded to fp16 first), up to 160 the narrow MFMA kernel in gate/up mode
+(k-splits hand partial tiles to the last split), above the wide-tile MFMA
+kernel (fp32 accumulators throughout).  Bar: max-abs-err <= 2e-2 * rms(ref),
+cosine >= 0.9999."""
 
 import numpy as np
 import pytest
@@ -56,6 +58,23 @@ def test_gate_up_swiglu_vs_oracle(m, k, n, K, cb):
     out = _run(x, tg, su, sg, tu, sv_u, K, cb)
     assert out.shape == (m, n) and out.dtype == torch.float16
     check_close(out.float().cpu().numpy(), _ref(x, tg, su, sg, tu, sv_u, K, cb, float("inf")), f"gate_up m={m}")
+
+
+@pytest.mark.parametrize("m,cb", [(5, 2), (13, 0), (40, 1), (100, 2), (150, 0), (160, 1)])
+def test_gate_up_split_handoff_ragged_rows(m, cb):
+    """The narrow kernel's gate/up k-splits (k = 2048: two splits of 16 steps,
+    n = 384: three column blocks per projection) on row counts that leave the
+    last row tile partial; bit-identical on a repeat call (the counters reset
+    themselves)."""
+    k, n, K = 2048, 384, 3
+    print(f"case: gate_up split hand-off ragged m={m} cb={cb}", flush=True)
+    tg, su, sg, tu, sv_u = _pair(k, n, K, seed=110 + m)
+    x = make_x(m, k, seed=111 + m)
+    first = _run(x, tg, su, sg, tu, sv_u, K, cb)
+    again = _run(x, tg, su, sg, tu, sv_u, K, cb)
+    assert torch.equal(first, again), "gate/up split hand-off: repeated calls differ"
+    check_close(first.float().cpu().numpy(), _ref(x, tg, su, sg, tu, sv_u, K, cb, float("inf")),
+                f"gate_up split hand-off m={m} cb={cb}")
 
 
 @pytest.mark.parametrize("m", [8, 200])
