@@ -167,12 +167,14 @@ size_t exl3_gate_up_workspace_size(int m, int k, int n, int K);
  * for both (src/sglang_exl3/exl3.py:1184-1206: exl3_fat_gemm over the
  * concatenated packs, then clamp, sigmoid * gate * up and the fp16 copy in
  * torch).  Trellis [k/16][n/16][16K] and svh f16 [n] per projection, one K
- * and codebook.  L = swiglu_limit; 0 or inf: no clamp.  Up to 64 rows the
+ * and codebook.  L = swiglu_limit; 0 or inf: no clamp.  Up to 3 rows the
  * gate/up GEMV kernel (g and u rounded to fp16 before the SwiGLU, as the
  * reference's batched decode path returns them, exl3.py:1018-1034); above,
- * the input is rotated once and the wide-tile MFMA kernel computes both
- * projections of a column block in one workgroup and applies the SwiGLU in
- * its epilogue (g and u in fp32).  Replaces the gate/up half of
+ * the input is rotated once and an MFMA kernel computes both projections of
+ * a column block and applies the SwiGLU in its epilogue (g and u in fp32):
+ * up to 160 rows the narrow kernel in gate/up mode (its k-splits hand fp32
+ * partial tiles to the last split of each column block and row tile), above
+ * it the wide-tile kernel, one workgroup holding the gate and up columns.  Replaces the gate/up half of
  * apply_exl3_batched_fat (src/sglang_exl3/exl3.py:1154-1206). */
 int exl3_gate_up_swiglu(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis,
                         const uint16_t* gate_svh, const int16_t* up_trellis, const uint16_t* up_svh,

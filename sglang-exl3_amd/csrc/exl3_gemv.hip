@@ -296,7 +296,7 @@ GemvParams base_params(const uint16_t* x, const int16_t* trellis, const uint16_t
     return p;
 }
 
-// --------------------------------------------------- dense gate + up (m <= 64)
+// ----------------------------- dense gate + up on the GEMV kernel (m <= 64)
 
 // Gate and up as the two "experts" of one k-split GEMV launch; the last of a
 // column block's 2 S workgroups applies the SwiGLU.  Scratch: counters (one

@@ -39,9 +39,10 @@ def _marker_on(t: Optional[torch.Tensor]) -> bool:
 def linear_forward(x2: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
                    codebook: int) -> torch.Tensor:
     """fp16 [rows, n] = x2 (fp16 [rows, k]) @ W for any codebook id, through the
-    registered op torch.ops.sglang_exl3.exl3_linear (exl3_gemv up to 64 rows,
-    exl3_gemm above; shapes checked there), so the call stays one traceable
-    op under torch.compile and graph capture."""
+    registered op torch.ops.sglang_exl3.exl3_linear (the C ABI's exl3_gemm: GEMV
+    kernels up to 12 rows, 8 from 12288 output columns, 7 from 24576, the MFMA
+    GEMM above; shapes checked there), so the call stays one traceable op
+    under torch.compile and graph capture."""
     from .ops import register_custom_ops
 
     register_custom_ops()
