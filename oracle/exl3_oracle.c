@@ -243,7 +243,9 @@ int orc_dequant(const uint16_t* trellis, const uint16_t* suh, const uint16_t* sv
 /* ---------------------------------------------------------------- matmul */
 
 /* y[m,n] = x[m,k] . W[k,n] with fp16 inputs, fp32 products and fp64
- * accumulation (a tighter reference than the reference's fp32 at::mm). */
+ * accumulation (a tighter reference than the reference's fp32 at::mm).
+ * A product of two fp16 values is exact in fp32.  Zero inputs are not
+ * skipped, so 0 * inf and 0 * NaN in W give NaN as IEEE arithmetic does. */
 void orc_matmul_f16(const uint16_t* x, const uint16_t* W, int m, int k, int n, float* y)
 {
     double* acc = (double*)calloc((size_t)n, sizeof(double));
@@ -252,7 +254,6 @@ void orc_matmul_f16(const uint16_t* x, const uint16_t* W, int m, int k, int n, f
         memset(acc, 0, (size_t)n * sizeof(double));
         for (int kk = 0; kk < k; ++kk) {
             float xv = orc_half_to_float(x[(size_t)i * k + kk]);
-            if (xv == 0.0f) continue;
             const uint16_t* wr = W + (size_t)kk * n;
             for (int j = 0; j < n; ++j) wrow[j] = orc_half_to_float(wr[j]);
             for (int j = 0; j < n; ++j) acc[j] += (double)(xv * wrow[j]);

@@ -216,6 +216,79 @@ def test_cpu_gemv_is_dequant_then_fp32_product():
     assert np.allclose(y, x.astype(np.float64) @ W, rtol=1e-4, atol=1e-3)
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 256, 384), (3, 640, 128), (17, 96, 200)])
+def test_matmul_matches_float64_numpy_product(m, k, n):
+    """oracle.matmul against numpy's float64 product of the same fp16 operands
+    (a different summation order and code).  Each fp16 x fp16 product is exact,
+    so the only error is fp64 accumulation (<= k eps64 sum|x||W|) plus the final
+    fp32 rounding (half an fp32 ulp).  k != n, so a transposed operand fails."""
+    rng = np.random.default_rng(100 + m)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    W = (rng.standard_normal((k, n)) * 3).astype(np.float16)
+    want = x.astype(np.float64) @ W.astype(np.float64)
+    got = oracle.matmul(x, W).astype(np.float64)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(W.astype(np.float64))
+    bound = 0.5 * np.spacing(np.abs(want).astype(np.float32)).astype(np.float64) + k * 2.0 ** -52 * mag
+    assert np.all(np.abs(got - want) <= bound)
+
+
+def test_matmul_one_hot_rows_select_weight_rows():
+    """x = e_i gives y = W[i, :] exactly; x = a e_i + b e_j gives a W_i + b W_j
+    (exact here: power-of-two coefficients)."""
+    rng = np.random.default_rng(21)
+    k, n = 48, 80
+    W = rng.standard_normal((k, n)).astype(np.float16)
+    idx = [0, 7, 47, 13]
+    x = np.zeros((len(idx) + 1, k), dtype=np.float16)
+    for r, i in enumerate(idx):
+        x[r, i] = 1.0
+    x[-1, 3], x[-1, 30] = 2.0, -0.25
+    y = oracle.matmul(x, W)
+    for r, i in enumerate(idx):
+        assert np.array_equal(y[r], W[i].astype(np.float32))
+    Wd = W.astype(np.float64)
+    assert np.array_equal(y[-1].astype(np.float64), 2.0 * Wd[3] - 0.25 * Wd[30])
+
+
+def test_matmul_propagates_inf_and_nan_like_ieee():
+    """A zero input times an inf or NaN weight is NaN (no zero-input shortcut);
+    a finite input times inf is inf; numpy's float64 product is the check."""
+    k, n = 8, 6
+    W = np.ones((k, n), dtype=np.float16)
+    W[2, 1] = np.inf
+    W[5, 4] = np.nan
+    x = np.ones((3, k), dtype=np.float16)
+    x[1, 2] = 0.0
+    x[2, 5] = 0.0
+    x[2, 2] = -1.0
+    with np.errstate(invalid="ignore"):
+        want = x.astype(np.float64) @ W.astype(np.float64)
+    got = oracle.matmul(x, W).astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin], want[fin])
+    assert np.isnan(got[1, 1]) and np.isnan(got[2, 4]) and got[2, 1] == -np.inf
+
+
+@pytest.mark.parametrize("cb,c", [(1, 1.84375), (2, -3.453125)])
+def test_linear_ref_zero_trellis_closed_form(cb, c):
+    """All-zero trellis through linear_ref (dequant then matmul): only the
+    (128i, 128j) corners of W are non-zero, so
+    y[128j] = 128 c svh[128j] sum_i x[128i] suh[128i] and y = 0 elsewhere."""
+    k, n, K = 384, 256, 3
+    rng = np.random.default_rng(31 + cb)
+    su = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+    sv = (np.where(rng.random(n) < 0.5, -1.0, 1.0) * 2.0 ** rng.integers(-2, 3, n)).astype(np.float16)
+    x = rng.standard_normal((5, k)).astype(np.float16)
+    y = oracle.linear_ref(x, np.zeros((k // 16, n // 16, 16 * K), dtype=np.int16), su, sv, K, cb).astype(np.float64)
+    s = (x[:, ::128].astype(np.float64) * su[::128].astype(np.float64)).sum(axis=1)
+    want = 128.0 * c * np.outer(s, sv[::128].astype(np.float64))
+    assert np.allclose(y[:, ::128], want, rtol=1e-6, atol=0)
+    mask = np.ones(n, dtype=bool)
+    mask[::128] = False
+    assert not y[:, mask].any()
+
+
 def test_swiglu_matches_torch_silu():
     """oracle.swiglu against torch's own SiLU (an independent implementation of
     silu(min(g, L)) * clamp(u, -L, L), src/sglang_exl3/exl3.py:572), on values
