@@ -5,9 +5,9 @@
  * stream).  Every device pointer must point into memory of the current HIP
  * device.  Every entry point returns EXL3_OK (0) or a non-zero status, and
  * exl3_last_error() then describes the failure (thread-local string).
- * Kernels are enqueued asynchronously on `stream`; no entry point
- * synchronises, allocates device memory or copies to the host, so all of them
- * can be captured into a HIP graph.
+ * Kernels are enqueued asynchronously on `stream`; no entry point but
+ * exl3_workspace_status synchronises, allocates device memory or copies to
+ * the host, so all the others can be captured into a HIP graph.
  *
  * Element types: "f16" = IEEE binary16 bits (uint16_t), "f32" = float,
  * trellis words = int16 as stored by EXL3 ([k/16][n/16][16*K] row-major).
@@ -33,6 +33,11 @@ extern "C" {
 #define EXL3_ERR_UNSUPPORTED 2 /* valid input outside the implemented set */
 #define EXL3_ERR_HIP 3         /* HIP runtime / launch failure */
 #define EXL3_ERR_WORKSPACE 4   /* workspace missing or too small */
+
+/* Bits of the workspace status word (exl3_workspace_status): a bounded wait
+ * inside a launch gave up, so that launch's output is not valid. */
+#define EXL3_WAIT_MOE_FUSED 1 /* one-launch one-token MoE: a down item's wait for its h blocks */
+#define EXL3_WAIT_FAT_TAIL 2  /* wide-tile GEMM tail split: the second k-half's wait for the first */
 
 #define EXL3_CB_3INST 0
 #define EXL3_CB_MCG 1
@@ -213,7 +218,9 @@ int exl3_moe_plan(int tokens, int topk, int num_experts, int hidden, int inter, 
  * skipped (weight ignored), like map_topk_to_local's invalid slot.  The nine
  * pointer tables are int64 device arrays of num_experts device addresses.
  * swiglu_limit <= 0 or infinite: no clamp.  K per projection 1..8, one
- * codebook; hidden, inter multiples of 128; tokens * topk <= 8192.
+ * codebook; hidden, inter multiples of 128; num_experts <= 4096, topk <=
+ * 16384, any number of tokens (batches above 8192 (token, slot) entries take
+ * the prefill path, which runs them in chunks of 16384 entries).
  * Replaces the routed-expert paths of EXL3MoEMethod.apply
  * (src/sglang_exl3/exl3.py:2253-2314 -> apply_exl3_experts :1347-1431 ->
  * apply_exl3_python_loop :520-576 / apply_exl3_batched_moe_gemv :960-1110). */
@@ -238,6 +245,19 @@ int exl3_p2b_fused_moe(const uint16_t* x, uint16_t* out, const int64_t* gate_tre
                        const uint16_t* routing_weights, int num_ids, int hidden, int inter, int K_gate,
                        int K_up, int K_down, int codebook, float swiglu_limit, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* Status word of a workspace: *status_out = the EXL3_WAIT_* bits set by
+ * launches on it since the last call (0: none), and the word is cleared.  A
+ * set bit means some launch's bounded wait gave up and its output is not
+ * valid; the workspace's counters may then be left non-zero, so zero the
+ * whole workspace before its next use.  Enqueues a 4-byte copy on `stream`
+ * and synchronises it, so it cannot be called during graph capture
+ * (EXL3_ERR_ARG).  workspace_bytes must cover the counter region (256 KiB).
+ * No counterpart in the reference, whose cooperative kernels wait without a
+ * bound (csrc/p2b_moe.cu:166-362, grid.sync) and exit the process on a
+ * launch error (csrc/util.cuh:92-100); for callers that need to know that a
+ * bounded wait gave up. */
+int exl3_workspace_status(void* workspace, size_t workspace_bytes, int32_t* status_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -36,11 +36,23 @@ inline int launch_status(const char* what) {
 // once; every kernel resets what it used).  Scratch starts at a fixed offset,
 // so no call's scratch ever overlaps the zeroed regions.
 constexpr size_t kWsCounterBytes = 256 * 1024;
-constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int);
+// Counters a call may use; the last 64 ints of the region are kept out of
+// counter use and hold the bounded-wait status word (kWsStatusIndex).
+constexpr size_t kWsMaxCounters = kWsCounterBytes / sizeof(int) - 64;
+// Status word (int index into the counter region): a kernel whose bounded
+// wait gave up ORs its EXL3_WAIT_* bit in; exl3_workspace_status reads and
+// clears it.
+constexpr size_t kWsStatusIndex = kWsCounterBytes / sizeof(int) - 1;
 
 constexpr size_t kWsAccOffset = kWsCounterBytes;
 constexpr size_t kWsAccBytes = 4 * 1024 * 1024;
 constexpr size_t kWsScratchOffset = kWsAccOffset + kWsAccBytes;
+
+// Polls a bounded wait makes before it gives up (each poll is followed by
+// ~0.2 us of s_sleep, so the default is ~0.25 s, far beyond any hand-off
+// inside one launch).  Env EXL3_WAIT_POLLS overrides it (tests set 0 to
+// make a wait give up from the host), clamped to [0, 2^24].
+constexpr int kWaitPolls = 1 << 20;
 
 // LDS a gfx950 workgroup may allocate.
 constexpr size_t kMaxLds = 160 * 1024;
@@ -58,6 +70,11 @@ inline int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     if (!v || !*v) return dflt;
     return atoi(v);
+}
+
+inline int wait_polls() {
+    const int v = env_int("EXL3_WAIT_POLLS", kWaitPolls);
+    return v < 0 ? 0 : (v > (1 << 24) ? (1 << 24) : v);
 }
 
 // exl3_gemm: GEMV kernels up to this many rows for outputs narrower than

@@ -44,3 +44,33 @@ int allow_dynamic_lds(const void* kernel, size_t need, const char* what) {
 extern "C" int exl3_abi_version(void) { return EXL3_ABI_VERSION; }
 
 extern "C" const char* exl3_last_error(void) { return exl3::g_err; }
+
+extern "C" int exl3_workspace_status(void* workspace, size_t workspace_bytes, int32_t* status_out, void* stream) {
+    using namespace exl3;
+    clear_error();
+    EXL3_REQUIRE(workspace && status_out, "exl3_workspace_status: null pointer");
+    EXL3_REQUIRE(workspace_bytes >= kWsCounterBytes, "exl3_workspace_status: workspace of %zu bytes has no status word",
+                 workspace_bytes);
+    hipStream_t st = as_stream(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+        set_error("exl3_workspace_status: cannot query the stream's capture state");
+        return EXL3_ERR_HIP;
+    }
+    EXL3_REQUIRE(cs == hipStreamCaptureStatusNone, "exl3_workspace_status: cannot run during graph capture");
+    int32_t* word = reinterpret_cast<int32_t*>(workspace) + kWsStatusIndex;
+    int32_t host = 0;
+    static const int32_t zero = 0;
+    if (hipMemcpyAsync(&host, word, sizeof(int32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        set_error("exl3_workspace_status: reading the status word failed");
+        return EXL3_ERR_HIP;
+    }
+    if (host != 0 && (hipMemcpyAsync(word, &zero, sizeof(int32_t), hipMemcpyHostToDevice, st) != hipSuccess ||
+                      hipStreamSynchronize(st) != hipSuccess)) {
+        set_error("exl3_workspace_status: clearing the status word failed");
+        return EXL3_ERR_HIP;
+    }
+    *status_out = host;
+    return EXL3_OK;
+}

@@ -217,6 +217,8 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
         p.tail_first = p.tiles_x * ((M + FB_ROWS - 1) / FB_ROWS) - tail;
         p.tail_part = reinterpret_cast<float*>(tail_part);
         p.tail_sync = tail_sync;
+        p.max_polls = wait_polls();
+        p.status = tail_sync + kWsStatusIndex;  // tail_sync is the workspace's counter region
     }
     p.a = reinterpret_cast<const __half*>(a);
     p.trellis = reinterpret_cast<const uint32_t*>(trellis);
@@ -395,6 +397,8 @@ int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate
             p.tail_first = p.tiles_x * ((m + FB_ROWS - 1) / FB_ROWS) - tail;
             p.tail_part = p.partials;
             p.tail_sync = p.counters;
+            p.max_polls = wait_polls();
+            p.status = p.counters + kWsStatusIndex;
         }
     }
     return fat_launch(K, cb, pl.mt, p, pl.splits, st);

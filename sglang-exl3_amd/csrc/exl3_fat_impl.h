@@ -106,6 +106,8 @@ struct FatParams {
     int tail_first, tail_tiles, tiles_x;
     float* tail_part;  // [tail_tiles][FB_TAIL_FLOATS]
     int* tail_sync;    // [tail_tiles] arrival counts, then [tail_tiles] flags; zero between calls
+    int max_polls;     // polls before the second half's wait gives up
+    int* status;       // workspace status word: EXL3_WAIT_FAT_TAIL when a wait gave up
     // Narrow kernel on mul1 weights (fat_gemm_kernel<.., RAW = true>, plain
     // and gate/up modes): B holds the raw entries (mul1_raw_pair) and the
     // epilogue applies kMul1Kinv * acc + kMul1Bias * (sum of the rows' x over
@@ -432,10 +434,6 @@ constexpr int FB_PASS_ROWS = 64;                // epilogue rows per LDS pass (3
 constexpr int FB_CTS = FB_COLS + 4;             // epilogue row stride (floats)
 constexpr int FAT_MT_WIDE = 0;                  // plan value (rows per tile) selecting fat_big_kernel
 constexpr int FB_TAIL_FLOATS = FB_ROWS * FB_COLS;  // one tile's fp32 accumulators (tail split)
-// Polls (each followed by an s_sleep of ~0.2 us) after which the second half
-// of a split tile stops waiting for the first (~0.25 s, far beyond a tile;
-// a bound so that every wave exits even if the first half never stored).
-constexpr int kFatTailPolls = 1 << 20;
 
 constexpr size_t fat_big_smem_bytes() {
     constexpr size_t stage = 2 * (size_t)FB_A_BYTES + 2 * (size_t)FB_B_BYTES;
@@ -669,10 +667,18 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
             return;
         }
         if (tid == 0) {
-            for (int it = 0; it < kFatTailPolls; ++it) {
-                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            // bounded (p.max_polls polls of ~0.2 us each) so that every wave
+            // exits even if the first half never stored; a wait that gives
+            // up is reported in the workspace status word
+            bool got = false;
+            for (int it = 0; it < p.max_polls; ++it) {
+                if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                    got = true;
+                    break;
+                }
                 __builtin_amdgcn_s_sleep(8);
             }
+            if (!got) report_wait_expired(p.status, EXL3_WAIT_FAT_TAIL);
             __hip_atomic_store(p.tail_sync + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

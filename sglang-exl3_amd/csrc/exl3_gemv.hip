@@ -312,6 +312,8 @@ size_t gate_up_gemv_bytes(int m, int k, int n, int K) {
 int run_gate_up_gemv(const uint16_t* x, const uint16_t* suh, const int16_t* gt, const uint16_t* gsv,
                      const int16_t* ut, const uint16_t* usv, uint16_t* out, int m, int k, int n, int K, int cb,
                      float limit, void* ws, size_t ws_bytes, hipStream_t st) {
+    EXL3_REQUIRE_CODE(m <= 16, EXL3_ERR_UNSUPPORTED, "exl3_gate_up_swiglu: the GEMV path takes at most 16 rows, not %d",
+                      m);
     const GemvPlan pl = plan_gate_up(m, k, n, K);
     const size_t need = gate_up_gemv_bytes(m, k, n, K);
     EXL3_REQUIRE_CODE(ws && ws_bytes >= need, EXL3_ERR_WORKSPACE,
@@ -343,6 +345,15 @@ int run_gate_up_gemv(const uint16_t* x, const uint16_t* suh, const int16_t* gt, 
 // 24.8-25.1 / 25.1-25.5 / 27.1 us (the GEMV workgroups each re-rotate all m
 // input rows of their k range).
 constexpr int kGateUpMaxGemvRows = 3;
+// The gate/up GEMV mode is instantiated for one MFMA row block only.
+constexpr int kGateUpGemvRowLimit = 16;
+
+// Rows up to which exl3_gate_up_swiglu takes the GEMV path: the default, or
+// env EXL3_GATE_UP_GEMV_ROWS clamped to [0, kGateUpGemvRowLimit].
+int gate_up_gemv_rows() {
+    const int r = env_int("EXL3_GATE_UP_GEMV_ROWS", kGateUpMaxGemvRows);
+    return r < 0 ? 0 : (r > kGateUpGemvRowLimit ? kGateUpGemvRowLimit : r);
+}
 
 size_t fat_gate_up_scratch_bytes(int m, int k, int n);
 int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis, const uint16_t* gate_svh,
@@ -355,7 +366,7 @@ using namespace exl3;
 
 extern "C" size_t exl3_gate_up_workspace_size(int m, int k, int n, int K) {
     if (m < 1 || k < 128 || n < 128 || k % 128 || n % 128 || K < 1 || K > 8) return 0;
-    const int gemv_rows = env_int("EXL3_GATE_UP_GEMV_ROWS", kGateUpMaxGemvRows);
+    const int gemv_rows = gate_up_gemv_rows();
     size_t need = m > gemv_rows ? fat_gate_up_scratch_bytes(m, k, n) : gate_up_gemv_bytes(m, k, n, K);
     if (m <= 64) {  // room for both paths (EXL3_GATE_UP_GEMV_ROWS moves the switch point)
         const size_t c = fat_gate_up_scratch_bytes(m, k, n), d = gate_up_gemv_bytes(m, k, n, K);
@@ -379,7 +390,7 @@ extern "C" int exl3_gate_up_swiglu(const uint16_t* x, const uint16_t* suh, const
     EXL3_REQUIRE(!(swiglu_limit < 0.0f) && swiglu_limit == swiglu_limit,
                  "exl3_gate_up_swiglu: swiglu_limit must be >= 0 (0 or inf: no clamp)");
     hipStream_t st = as_stream(stream);
-    if (m > env_int("EXL3_GATE_UP_GEMV_ROWS", kGateUpMaxGemvRows))
+    if (m > gate_up_gemv_rows())
         return fat_gate_up_rows(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, out, m, k, n, K, codebook,
                                 swiglu_limit, workspace, workspace_bytes, st);
     return run_gate_up_gemv(x, suh, gate_trellis, gate_svh, up_trellis, up_svh, out, m, k, n, K, codebook,

@@ -103,6 +103,12 @@ __device__ __forceinline__ float2 coherent_load2(const float* p) {
     return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
 }
 
+// A bounded wait gave up: OR `bit` (EXL3_WAIT_*) into the workspace status
+// word, where exl3_workspace_status finds it.
+__device__ __forceinline__ void report_wait_expired(int* status, int bit) {
+    __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 constexpr int GV_MAX_SPLITS = 16;  // k-splits a reduction reads in one round trip
 
 // sum_{s < S} p[s * stride] in split order.  The S device-coherent loads are

@@ -543,7 +543,7 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     if (ready_stride < inter / 128) ready_stride = inter / 128;
     const bool fused = direct && KG == KU && KU == KD && moe_fused_steps_ok(L.gu.ns) && moe_fused_steps_ok(L.dn.ns) &&
                        L.gu.kw == 1 && L.dn.kw == 1 &&
-                       (size_t)topk * (inter / 128 + hidden / 128 + ready_stride + 1) + 256 <= kWsMaxCounters &&
+                       (size_t)topk * (inter / 128 + hidden / 128 + ready_stride + 1) + 258 <= kWsMaxCounters &&
                        env_int("EXL3_MOE_FUSED", 0) != 0;
 
     // 3. gate + up (+ SwiGLU + down input rotation)
@@ -562,11 +562,15 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     pg.proj_base = 0;
     pg.proj_launch = 2;
     if (fused) {
-        // counters: [gate/up hand-off | down hand-off | readiness flags | done counts]
+        // counters: [gate/up hand-off | down hand-off | readiness flags | done
+        // counts | item ticket, finished workgroups]
         const int nbg = inter / 128, nbd = hidden / 128;
         int* c0 = reinterpret_cast<int*>(w8);
         pg.ready = c0 + (((size_t)topk * (nbg + nbd) + 255) & ~(size_t)255);
         pg.done = pg.ready + (size_t)topk * ready_stride;
+        pg.ticket = pg.done + topk;
+        pg.max_polls = wait_polls();
+        pg.status = c0 + kWsStatusIndex;
         pg.ready_nblk = nbg;
         pg.ready_stride = ready_stride;
         pg.poll_sleep = env_int("EXL3_MOE_POLL_SLEEP", 1);
@@ -618,6 +622,9 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
         p.ready_stride = pg.ready_stride;
         p.poll_sleep = pg.poll_sleep;
         p.prime_late = pg.prime_late;
+        p.max_polls = pg.max_polls;
+        p.status = pg.status;
+        p.ticket = pg.ticket;
         p.dn_items_per_unit = ((hidden / 128) / L.dn.bpi) * L.dn.splits;
         rc = moe_fused_launch(KD, cb, L.gu.ns, L.dn.ns, pg, p, st);
     } else {

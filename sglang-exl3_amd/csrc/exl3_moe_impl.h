@@ -126,6 +126,13 @@ struct MoeParams {
     // into the token's fixed-point accumulators, which complete after
     // valid-slots x splits contributions (the output rotation is linear).
     int fxs;
+    // Bounded waits (fused one-token launch): polls before a wait gives up,
+    // and the workspace status word that then gets EXL3_WAIT_MOE_FUSED; the
+    // launch's tickets (next item, finished workgroups) in the zeroed
+    // counter region.
+    int max_polls;
+    int* status;
+    int* ticket;
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
@@ -159,20 +166,19 @@ __device__ __forceinline__ void st_h2_coherent(EXL3_GLOBAL __half* ptr, __half2 
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls (each followed by an s_sleep of ~0.2 us) after which a fused down item
-// stops waiting for its h blocks (about 0.25 s: far beyond any gate/up pass;
-// a bound so that every wave exits even if a producer never ran).
-constexpr int kMoeWaitPolls = 1 << 20;
-
-// Wait until the readiness flags f[j0..j1] are all set (one thread).
-__device__ __forceinline__ void wait_ready(const int* f, int j0, int j1, int nsleep) {
-    for (int it = 0; it < kMoeWaitPolls; ++it) {
+// Wait until the readiness flags f[j0..j1] are all set (one thread), for at
+// most max_polls polls (each followed by nsleep s_sleep(8) calls, ~0.2 us
+// each): a bound so that every wave exits even if a producer never ran.
+// Returns false when the wait gave up.
+__device__ __forceinline__ bool wait_ready(const int* f, int j0, int j1, int nsleep, int max_polls) {
+    for (int it = 0; it < max_polls; ++it) {
         bool ok = true;
         for (int j = j0; j <= j1; ++j)
             ok = ok && __hip_atomic_load(const_cast<int*>(f) + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-        if (ok) return;
+        if (ok) return true;
         for (int z = 0; z < nsleep; ++z) __builtin_amdgcn_s_sleep(8);
     }
+    return false;
 }
 
 // Valid slots of a directly routed token (ids in [0, E)).
@@ -310,8 +316,9 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     uint32_t w[gv_depth<K>()][K];
     if constexpr (wait_h) {
         if (!p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
-        if (tid == 0)
-            wait_ready(p.ready + (size_t)u * p.ready_stride, kt_wg0 >> 3, (kt_wg0 + kts_wg - 1) >> 3, p.poll_sleep);
+        if (tid == 0 && !wait_ready(p.ready + (size_t)u * p.ready_stride, kt_wg0 >> 3, (kt_wg0 + kts_wg - 1) >> 3,
+                                    p.poll_sleep, p.max_polls))
+            report_wait_expired(p.status, EXL3_WAIT_MOE_FUSED);
         __syncthreads();
         if (p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
         preload();
@@ -640,16 +647,18 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
 }
 
 // One token routed directly, gate/up and down in one persistent launch.
-// Items [0, Ngu) are the gate/up items, [Ngu, Ngu + Ndn) the down items
-// (index order = the order every workgroup takes its items in).  A down item
-// requests its weights at once and then waits (bounded) for the h blocks of
-// its k range, which the gate/up epilogues publish.  Forward progress: the
-// grid is the number of workgroups the device holds at once, so every item
-// has a running workgroup; a workgroup's gate/up items all precede its down
-// items, and gate/up items never wait, so every awaited block is produced.
+// Items [0, Ngu) are the gate/up items, [Ngu, Ngu + Ndn) the down items.
+// Workgroups claim items from a ticket counter (pg.ticket[0], zero between
+// calls), so items are taken in index order: a down item, which requests its
+// weights at once and then waits (bounded) for the h blocks of its k range,
+// only ever waits for gate/up items that running workgroups already hold,
+// and gate/up items never wait, so every awaited block is produced whether
+// or not all workgroups of the grid are resident.  The last workgroup to
+// finish (pg.ticket[1] counts them) resets both counters for the next call.
 template <int K, int CB, int NSG, int NSD>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(MoeParams pg, MoeParams pd) {
     extern __shared__ __align__(16) unsigned char mv_smem[];
+    __shared__ int claimed;
     const int direct_valid = direct_valid_slots(pd);
     if (direct_valid == 0) {
         if (blockIdx.x == 0 && pd.fc) zero_row(pd.final_out, pd.n);
@@ -657,10 +666,19 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
     }
     const int ngu = pg.topk * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits;
     const int total = ngu + pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
-    const int G = gridDim.x, b0 = blockIdx.x;
-    for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0)) {
+    for (int rnd = 0;; ++rnd) {
+        if (threadIdx.x == 0) claimed = __hip_atomic_fetch_add(pg.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int it = claimed;
+        __syncthreads();
+        if (it >= total) break;
         if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true>(pg, it, mv_smem, direct_valid, rnd == 0);
         else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true>(pd, it - ngu, mv_smem, direct_valid, rnd == 0);
+    }
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(pg.ticket + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
+        __hip_atomic_store(pg.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pg.ticket + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

@@ -19,6 +19,10 @@ EXL3_ERR_UNSUPPORTED = 2
 EXL3_ERR_HIP = 3
 EXL3_ERR_WORKSPACE = 4
 
+# bits of the workspace status word (exl3_workspace_status)
+EXL3_WAIT_MOE_FUSED = 1
+EXL3_WAIT_FAT_TAIL = 2
+
 CB_3INST = 0
 CB_MCG = 1
 CB_MUL1 = 2
@@ -53,6 +57,7 @@ SIGNATURES = {
                             _I, _I, _I, _I, _F, _P, _SZ, _P]),
     "exl3_p2b_fused_moe": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I,
                                 _I, _I, _I, _I, _F, _P, _SZ, _P]),
+    "exl3_workspace_status": (_I, [_P, _SZ, _P, _P]),
 }
 
 _lib = None

@@ -35,9 +35,13 @@ OP_NAMES = (
 # ---------------------------------------------------------------- plumbing
 
 _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
-# Buffers replaced by a larger one.  A HIP graph captured earlier may still
-# hold their addresses, so they are never freed (a replay would otherwise
-# write counters and partial sums into memory that another tensor owns).
+# Buffers some HIP graph was captured with (by id; the dict keeps them alive,
+# so an id cannot be reused while it is listed).  A replay writes counters
+# and partial sums into the captured addresses, so such a buffer is kept when
+# a larger one replaces it (in _RETIRED_WORKSPACES, with its (device, stream)
+# key); a replaced buffer that no graph captured is dropped and freed
+# (stream-ordered, on the stream it was used on).
+_CAPTURED: Dict[int, torch.Tensor] = {}
 _RETIRED_WORKSPACES: list = []
 
 
@@ -67,17 +71,59 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     an uninitialised buffer.  Run each op shape once before capture."""
     key = (device.index or 0, int(torch.cuda.current_stream(device).cuda_stream))
     ws = _WORKSPACES.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
     if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
+        if capturing:
             raise RuntimeError(
                 f"sglang_exl3: the workspace of this stream must grow to {nbytes} bytes during HIP graph "
                 "capture; run the op once (same shape) on this stream before capturing")
         size = max(nbytes, 1 << 20, 0 if ws is None else 2 * ws.numel())
-        if ws is not None:
-            _RETIRED_WORKSPACES.append(ws)
+        if ws is not None and id(ws) in _CAPTURED:
+            _RETIRED_WORKSPACES.append((key, ws))
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
+    elif capturing:
+        _CAPTURED[id(ws)] = ws
     return ws
+
+
+WAIT_CAUSES = {
+    _lib.EXL3_WAIT_MOE_FUSED: "a down item of the one-launch one-token MoE layer (EXL3_MOE_FUSED=1) stopped "
+                              "waiting for its h blocks",
+    _lib.EXL3_WAIT_FAT_TAIL: "the second k-half of a wide-tile GEMM tail tile stopped waiting for the first",
+}
+
+
+def check_waits(device=None) -> None:
+    """Raise RuntimeError if a bounded wait inside a launch on one of this
+    process's workspaces of `device` (default: the current device) gave up
+    since the last check: that launch's output is not valid.  The kernels'
+    waits are bounded (about 0.25 s) so that every wave exits; a wait that
+    gives up sets a bit of the workspace's status word instead of failing
+    silently.  Synchronises the device; not callable during graph capture.
+    A workspace whose status was set is zeroed before the error is raised
+    (its counters may have been left non-zero), so later calls run clean."""
+    import ctypes
+
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    torch.cuda.synchronize(idx)
+    bits = 0
+    bufs = [(k, w) for k, w in _WORKSPACES.items() if k[0] == idx]
+    bufs += [(k, w) for k, w in _RETIRED_WORKSPACES if k[0] == idx]
+    with torch.cuda.device(idx):
+        for _, ws in bufs:
+            st = ctypes.c_int32(0)
+            rc = _lib.lib().exl3_workspace_status(ws.data_ptr(), ws.numel(), ctypes.byref(st), None)
+            _lib.check(rc, "exl3_workspace_status")
+            if st.value:
+                ws.zero_()
+                bits |= st.value
+        torch.cuda.synchronize(idx)
+    if bits:
+        what = "; ".join(v for b, v in WAIT_CAUSES.items() if bits & b) or f"status bits {bits:#x}"
+        raise RuntimeError(f"sglang_exl3: a bounded wait gave up ({what}); the outputs of the calls since the "
+                           "last check_waits() are not valid")
 
 
 def check_ws(rc: int, what: str, ws) -> None:

@@ -165,3 +165,15 @@ def test_gemv_noalloc_refuses_shapes_beyond_its_scratch():
     rc = L.exl3_gemv_noalloc(16, 16, 16, 16, 16, 64, 4096, 65536, 4, 1, None)
     assert rc == _lib.EXL3_ERR_UNSUPPORTED
     assert b"above the fixed" in L.exl3_last_error()
+
+
+def test_workspace_status_rejects_bad_arguments_without_a_gpu():
+    import ctypes
+
+    L = _lib.lib()
+    st = ctypes.c_int32(0)
+    assert L.exl3_workspace_status(None, 1 << 20, ctypes.byref(st), None) == _lib.EXL3_ERR_ARG
+    assert b"null pointer" in L.exl3_last_error()
+    assert L.exl3_workspace_status(16, 1 << 20, None, None) == _lib.EXL3_ERR_ARG
+    assert L.exl3_workspace_status(16, 1024, ctypes.byref(st), None) == _lib.EXL3_ERR_ARG
+    assert b"no status word" in L.exl3_last_error()
