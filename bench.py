@@ -596,7 +596,10 @@ def main():
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "tokens_per_s": round(1.0 / t1, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": ("profiles/gemv_cfg2_m1_traffic.txt: rocprofv3 FETCH_SIZE + WRITE_SIZE of "
+                                        "this kernel from a profiled run (bench.py --profile-pass gemv), not "
+                                        "measured in this run") if traffic is not None else None},
         "gemv_sweep": sweep,
     }
     if not args.no_extra:
