@@ -202,18 +202,27 @@ __device__ __forceinline__ FxPair fx_issue_pair(unsigned long long* acc, float a
 }
 
 // The add that brought an element to `cnt` contributions stores it to y
-// (fp16) and clears the accumulator for the next call.
+// (fp16) and clears the accumulator for the next call.  Both returned values
+// are read before any store, and when one add completed both elements (the
+// usual case: the last workgroup of a column block completes its pair) the
+// two fp16 values go out as one 4-byte store.  Storing the first element
+// before reading the second had the wave wait for that store's round trip
+// too (config 2 m = 1: 10.97 -> 10.64 us).
 __device__ __forceinline__ void fx_finish_pair(const FxPair& f, unsigned long long* acc, int cnt,
                                                EXL3_GLOBAL __half* y) {
-    if ((int)(f.oa >> SK_CNT_SHIFT) == cnt - 1) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y) = __half_as_ushort(__float2half_rn(sk_decode(f.oa + f.ea, cnt)));
-        __hip_atomic_store(acc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool ca = (int)(f.oa >> SK_CNT_SHIFT) == cnt - 1;
+    const bool cb = (int)(f.ob >> SK_CNT_SHIFT) == cnt - 1;
+    if (!(ca || cb)) return;
+    const float va = sk_decode(f.oa + f.ea, cnt), vb = sk_decode(f.ob + f.eb, cnt);
+    if (ca && cb) {
+        st_h2(y, __floats2half2_rn(va, vb));
+    } else if (ca) {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y) = __half_as_ushort(__float2half_rn(va));
+    } else {
+        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + 1) = __half_as_ushort(__float2half_rn(vb));
     }
-    if ((int)(f.ob >> SK_CNT_SHIFT) == cnt - 1) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + 1) =
-            __half_as_ushort(__float2half_rn(sk_decode(f.ob + f.eb, cnt)));
-        __hip_atomic_store(acc + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (ca) __hip_atomic_store(acc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cb) __hip_atomic_store(acc + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void fx_add_pair(unsigned long long* acc, float a, float b, int cnt, EXL3_GLOBAL __half* y) {

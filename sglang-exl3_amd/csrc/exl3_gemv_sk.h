@@ -119,9 +119,12 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
     const size_t ss = (size_t)4 * ntiles * (8 * K);  // words between k-steps
     const EXL3_GLOBAL uint32_t* tb = gptr(p.trellis) + ((size_t)(ks0 * 4 + g) * ntiles + nt) * (8 * K) + K * q;
     const __half2 svv = ld_h2(gptr(p.svh) + cb * 128 + 2 * lane);
+    // only the first step's words now; the rest of the ring after the
+    // staging barrier, so that the burst every wave issues at its start is
+    // one step (7.3 MB over the grid at config 2, not 14.7) and the decode
+    // starts sooner (config 2 m = 1: 10.64 -> 10.43 us)
     uint32_t w[D][K];
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_words<K>(tb + (size_t)(d < NS ? d : NS - 1) * ss, w[d]);
+    load_words<K>(tb, w[0]);
 
     // 2. input rotation into LDS (A order, each value duplicated).  A lane
     //    holds k = 128 j + 2 lane (+1): k-step 2j + lane/32, offset (2 lane) % 64
@@ -159,6 +162,8 @@ __global__ __launch_bounds__(SK_THREADS) void gemv_sk_kernel(GemvSkParams p) {
         }
     }
     __syncthreads();
+#pragma unroll
+    for (int d = 1; d < D; ++d) load_words<K>(tb + (size_t)(d < NS ? d : NS - 1) * ss, w[d]);
 
     // 3. decode + MFMA; four accumulator chains (quarter parity x column tile).
     //    Activation row r is A row r: lanes with i = r < m read it, the

@@ -648,13 +648,19 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
 
 // One token routed directly, gate/up and down in one persistent launch.
 // Items [0, Ngu) are the gate/up items, [Ngu, Ngu + Ndn) the down items.
-// Workgroups claim items from a ticket counter (pg.ticket[0], zero between
-// calls), so items are taken in index order: a down item, which requests its
-// weights at once and then waits (bounded) for the h blocks of its k range,
-// only ever waits for gate/up items that running workgroups already hold,
-// and gate/up items never wait, so every awaited block is produced whether
-// or not all workgroups of the grid are resident.  The last workgroup to
-// finish (pg.ticket[1] counts them) resets both counters for the next call.
+// Workgroup b takes item b first; when the grid is smaller than the item
+// count, further items come from a ticket counter (pg.ticket[0], zero
+// between calls) starting at the grid size, so items are taken in index
+// order and the last workgroup to finish (pg.ticket[1] counts them) resets
+// both counters.  A down item requests its weights at once and then waits
+// (bounded) for the h blocks of its k range, which gate/up items (never
+// waiting) publish.  Forward progress: a claimed item's gate/up producers
+// were claimed earlier; a first-round item's producers are the first items
+// of lower-numbered workgroups, which the grid (sized to the workgroups the
+// device holds at once) has running beside it.  If other work keeps some of
+// them from being resident, the wait gives up and sets EXL3_WAIT_MOE_FUSED in
+// the workspace status word.  (Claiming every item from the ticket measured
+// 38.4 against 22 us on config 4 B = 1: 768 contended atomics on one word.)
 template <int K, int CB, int NSG, int NSD>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(MoeParams pg, MoeParams pd) {
     extern __shared__ __align__(16) unsigned char mv_smem[];
@@ -666,17 +672,19 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
     }
     const int ngu = pg.topk * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits;
     const int total = ngu + pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
-    for (int rnd = 0;; ++rnd) {
-        if (threadIdx.x == 0) claimed = __hip_atomic_fetch_add(pg.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        const int it = claimed;
-        __syncthreads();
-        if (it >= total) break;
+    const int G = gridDim.x;
+    for (int rnd = 0, it = blockIdx.x; it < total; ++rnd) {
         if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true>(pg, it, mv_smem, direct_valid, rnd == 0);
         else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true>(pd, it - ngu, mv_smem, direct_valid, rnd == 0);
+        if (G >= total) break;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            claimed = G + __hip_atomic_fetch_add(pg.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        it = claimed;
     }
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(pg.ticket + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
+    if (G < total && threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(pg.ticket + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1) {
         __hip_atomic_store(pg.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(pg.ticket + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
