@@ -526,6 +526,7 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.counters = reinterpret_cast<int*>(w8);
     p.partials = reinterpret_cast<float*>(w8 + L.part_off);
     p.direct = direct;
+    p.tab_prefetch = env_int("EXL3_MOE_TAB_PREFETCH", 1) != 0;
     p.ids = ids;
     p.E = E;
     p.tabs = tb;

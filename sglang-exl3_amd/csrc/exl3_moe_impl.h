@@ -133,6 +133,9 @@ struct MoeParams {
     int max_polls;
     int* status;
     int* ticket;
+    // Directly routed items load their pointer-table entries for every
+    // expert beside the routed id (up to kDirectTabExperts experts)
+    int tab_prefetch;
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
@@ -179,6 +182,32 @@ __device__ __forceinline__ bool wait_ready(const int* f, int j0, int j1, int nsl
         for (int z = 0; z < nsleep; ++z) __builtin_amdgcn_s_sleep(8);
     }
     return false;
+}
+
+// Experts up to which a directly routed item loads its pointer-table entries
+// for every expert alongside the routed id (4 per lane).
+constexpr int kDirectTabExperts = 256;
+
+// Entries lane, lane + 64, lane + 128, lane + 192 of a pointer table (0 past E).
+struct TabRow {
+    unsigned long long v0, v1, v2, v3;
+};
+__device__ __forceinline__ TabRow tab_row(const int64_t* t, int E, int lane) {
+    const EXL3_GLOBAL int64_t* g = gptr(t);
+    TabRow r;
+    r.v0 = lane < E ? (unsigned long long)g[lane] : 0ull;
+    r.v1 = lane + 64 < E ? (unsigned long long)g[lane + 64] : 0ull;
+    r.v2 = lane + 128 < E ? (unsigned long long)g[lane + 128] : 0ull;
+    r.v3 = lane + 192 < E ? (unsigned long long)g[lane + 192] : 0ull;
+    return r;
+}
+// Entry e (uniform, < 256) of a TabRow, as a wave-uniform pointer.
+__device__ __forceinline__ const void* tab_pick(const TabRow& r, int e) {
+    const int s = e >> 6;
+    const unsigned long long v = s == 0 ? r.v0 : (s == 1 ? r.v1 : (s == 2 ? r.v2 : r.v3));
+    const unsigned lo = __builtin_amdgcn_readlane((unsigned)v, e & 63);
+    const unsigned hi = __builtin_amdgcn_readlane((unsigned)(v >> 32), e & 63);
+    return reinterpret_cast<const void*>(((unsigned long long)hi << 32) | lo);
 }
 
 // Valid slots of a directly routed token (ids in [0, E)).
@@ -247,16 +276,28 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     int m, crow0;
     const void *tp, *suh, *ev0p, *ev1p, *ev2p;
     if (direct) {
+        // Up to kDirectTabExperts experts, the table entries this item reads
+        // are requested for every expert (entry lane + 64 s in lane `lane`)
+        // together with the routed id, so the weight and sign-vector loads
+        // wait for one round trip instead of two (id, then entry).
+        const bool pre = p.tab_prefetch && p.E <= kDirectTabExperts;
+        const TabRow r0 = pre ? tab_row(p.tabs.t[pb], p.E, lane) : TabRow{};
+        const TabRow r1 = pre ? tab_row(p.tabs.t[pb + 1], p.E, lane) : TabRow{};
+        const TabRow r2 = pre ? tab_row(p.tabs.t[down ? 8 : 2], p.E, lane) : TabRow{};
+        const TabRow r3 = (pre && !down) ? tab_row(p.tabs.t[5], p.E, lane) : TabRow{};
+        const TabRow r4 = (pre && !down) ? tab_row(p.tabs.t[7], p.E, lane) : TabRow{};
         const int e = uniform_i(gptr(p.ids)[u]);
         if (e < 0 || e >= p.E) return;  // skipped slot (uniform over the workgroup)
         m = 1;
         crow0 = u;
-        auto tab = [&](int j) { return uniform_p(reinterpret_cast<const void*>(gptr(p.tabs.t[j])[e])); };
-        tp = tab(pb);
-        suh = tab(pb + 1);
-        ev0p = tab(down ? 8 : 2);
-        ev1p = tab(5);
-        ev2p = tab(7);
+        auto tab = [&](const TabRow& r, int j) -> const void* {
+            return pre ? tab_pick(r, e) : uniform_p(reinterpret_cast<const void*>(gptr(p.tabs.t[j])[e]));
+        };
+        tp = tab(r0, pb);
+        suh = tab(r1, pb + 1);
+        ev0p = tab(r2, down ? 8 : 2);
+        ev1p = down ? nullptr : tab(r3, 5);
+        ev2p = down ? nullptr : tab(r4, 7);
     } else {
         const EXL3_GLOBAL MoeUnit* ud = gptr(p.rt.units) + u;
         m = uniform_i(ud->nrows);
