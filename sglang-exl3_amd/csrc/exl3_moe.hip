@@ -445,8 +445,10 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     // Env EXL3_MOE_FC_TOKENS overrides the threshold (0: never fused).
     const int fc_tokens = env_int("EXL3_MOE_FC_TOKENS", kMoeFusedCombineTokens);
     L.fc = tokens <= fc_tokens && (size_t)tokens * hidden * 8 <= kWsAccBytes && topk <= SK_MAX_CONTRIB;
+    // h: the rotated activation rows; one token: room for the fp16 gate and up
+    // rows of the split fixed-point gate/up pass instead
     L.h_off = o;
-    o = align256(o + (size_t)L.entries * inter * 2);
+    o = align256(o + (size_t)(tokens == 1 ? 2 : 1) * L.entries * inter * 2);
     L.y_off = o;
     o = align256(o + (size_t)L.entries * hidden * 2);
     L.rot = tokens >= env_int("EXL3_MOE_ROT_TOKENS", kMoeRotTokens);
@@ -547,7 +549,26 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
                        (size_t)topk * (inter / 128 + hidden / 128 + ready_stride + 1) + 258 <= kWsMaxCounters &&
                        env_int("EXL3_MOE_FUSED", 0) != 0;
 
-    // 3. gate + up (+ SwiGLU + down input rotation)
+    // the fused combine one round trip per split (each split adds its rotated
+    // partial rows into the output accumulators) when every token's count of
+    // contributions (valid slots x splits) fits the accumulators' count bits
+    const bool dn_fxs = L.fc && L.dn.kw == 1 && topk * L.dn.splits <= SK_MAX_CONTRIB && env_int("EXL3_MOE_FXS", 1) != 0;
+    // One token in two launches: gate/up by split fixed-point adds (no
+    // partial rows, counter or last arrival; each element's completing add
+    // writes the fp16 gate or up value), and the down pass stages the SwiGLU
+    // from those rows, rotated with its own suh.  The split hand-off being one
+    // round trip, the gate/up items are cut finer (env EXL3_MOE_GFX_GU_NSTEPS,
+    // default 4 steps).  Env EXL3_MOE_GFX=0 keeps the partial-row hand-off.
+    const int gu_kslices = hidden / 16;
+    const int gfx_ns = env_int("EXL3_MOE_GFX_GU_NSTEPS", 4);
+    const bool gfx = direct && !fused && dn_fxs && moe_gfx_steps_ok(gfx_ns) && moe_gfx_steps_ok(L.dn.ns) &&
+                     gu_kslices % (4 * gfx_ns) == 0 && gu_kslices / (4 * gfx_ns) <= SK_MAX_CONTRIB &&
+                     ((size_t)tokens * hidden + (size_t)2 * L.entries * inter) * 8 <= kWsAccBytes &&
+                     env_int("EXL3_MOE_GFX", 1) != 0;
+    const int gu_ns = gfx ? gfx_ns : L.gu.ns;
+    unsigned long long* const acc_base = reinterpret_cast<unsigned long long*>(w8 + kWsAccOffset);
+
+    // 3. gate + up (+ SwiGLU + down input rotation; GFX: the gate and up rows)
     p.mode = MOE_GATE_UP;
     p.x = L.rot ? xr : reinterpret_cast<const __half*>(x);
     p.in_rot = L.rot;
@@ -555,7 +576,10 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.k = hidden;
     p.n = inter;
     p.nproj = 2;
-    p.splits = L.gu.splits;
+    p.splits = gfx ? gu_kslices / (4 * gfx_ns) : L.gu.splits;
+    p.gfx = gfx;
+    p.fxs = gfx;
+    if (gfx) p.acc = acc_base + (size_t)tokens * hidden;  // [2][entries][inter], after the output's
     p.kw = L.gu.kw;
     p.bx_per_item = L.gu.bpi;
     int rc;
@@ -579,15 +603,15 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     } else if (KG == KU) {
         p.proj_base = 0;
         p.proj_launch = 2;
-        rc = moe_launch(KG, cb, L.gu.ns, p, st);
+        rc = moe_launch(KG, cb, gu_ns, p, st);
         if (rc) return rc;
     } else {
         p.proj_launch = 1;
         p.proj_base = 0;
-        rc = moe_launch(KG, cb, L.gu.ns, p, st);
+        rc = moe_launch(KG, cb, gu_ns, p, st);
         if (rc) return rc;
         p.proj_base = 1;
-        rc = moe_launch(KU, cb, L.gu.ns, p, st);
+        rc = moe_launch(KU, cb, gu_ns, p, st);
         if (rc) return rc;
     }
 
@@ -605,15 +629,12 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.kw = L.dn.kw;
     p.bx_per_item = L.dn.bpi;
     p.fc = L.fc;
-    p.acc = reinterpret_cast<unsigned long long*>(w8 + kWsAccOffset);
+    p.acc = acc_base;
     p.tok_valid = tok_valid;
     p.weights = weights;
     p.weights_f16 = weights_f16;
     p.final_out = reinterpret_cast<__half*>(out);
-    // the fused combine one round trip per split (each split adds its rotated
-    // partial rows into the output accumulators) when every token's count of
-    // contributions (valid slots x splits) fits the accumulators' count bits
-    p.fxs = L.fc && L.dn.kw == 1 && topk * L.dn.splits <= SK_MAX_CONTRIB && env_int("EXL3_MOE_FXS", 1) != 0;
+    p.fxs = dn_fxs;
     if (fused) {
         p.counters = reinterpret_cast<int*>(w8) + (size_t)topk * (inter / 128);
         p.partials = reinterpret_cast<float*>(w8 + L.part_dn_off);

@@ -136,6 +136,14 @@ struct MoeParams {
     // Directly routed items load their pointer-table entries for every
     // expert beside the routed id (up to kDirectTabExperts experts)
     int tab_prefetch;
+    // Gate/up by split fixed-point adds (gfx != 0, moe_gemv_kernel<.., FXS =
+    // true, GFX = true>): each k-split item rotates and scales its partial
+    // rows and adds svh * H(partial) / sqrt(128) into acc[proj][crow][n]; the
+    // add completing an element (S contributions) writes the fp16 gate or up
+    // output to out[proj][crow][n] and clears it.  The down pass (GFX = true)
+    // then stages fp16(silu(min(g, L)) * clamp(u, -L, L)), rotated with its
+    // own suh, from those rows.
+    int gfx;
 };
 
 inline size_t moe_route_smem_bytes(int E, int entries, int tokens) {
@@ -167,6 +175,19 @@ __device__ __forceinline__ __half2 ld_h2_coherent(const EXL3_GLOBAL __half* ptr)
 __device__ __forceinline__ void st_h2_coherent(EXL3_GLOBAL __half* ptr, __half2 v) {
     __hip_atomic_store(reinterpret_cast<uint32_t*>((__half*)ptr), *reinterpret_cast<const uint32_t*>(&v),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// fp16(silu(min(g, L)) * clamp(u, -L, L)) of an fp16 gate and up pair (no
+// clamp when L <= 0 or infinite).
+__device__ __forceinline__ __half2 swiglu_h2(__half2 g, __half2 u, float limit) {
+    float g0 = __low2float(g), g1 = __high2float(g), u0 = __low2float(u), u1 = __high2float(u);
+    if (limit > 0.0f && limit < __builtin_huge_valf()) {
+        g0 = fminf(g0, limit);
+        g1 = fminf(g1, limit);
+        u0 = fminf(fmaxf(u0, -limit), limit);
+        u1 = fminf(fmaxf(u1, -limit), limit);
+    }
+    return h2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
 }
 
 // Wait until the readiness flags f[j0..j1] are all set (one thread), for at
@@ -234,7 +255,7 @@ __device__ __forceinline__ void zero_row(__half* out, int n) {
 // the LDS of a previous one).  FUSED: the gate/up and down passes share one
 // launch (moe_fused_direct_kernel): gate/up epilogues publish each finished
 // 128-wide block of h, and down items wait for the blocks they read.
-template <int K, int CB, int NS, int MODE, int KW, bool FUSED, bool FXS = false>
+template <int K, int CB, int NS, int MODE, int KW, bool FUSED, bool FXS = false, bool GFX = false>
 __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned char* mv_smem, int direct_valid,
                                          bool first) {
     constexpr int ROWS = MOE_UNIT_ROWS;
@@ -254,7 +275,9 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     const int cw = wave & 3, kwi = wave >> 2;
     const int g = lane >> 4, i = lane & 15, q = i & 7;
     constexpr bool down = MODE == MV_DOWN || MODE == MV_DOWN_DIRECT;
-    constexpr bool pre_rotated = MODE != MV_GU && MODE != MV_GU_DIRECT;  // input rows arrive rotated
+    // input rows arrive rotated (a GFX down pass rotates the SwiGLU it stages)
+    constexpr bool pre_rotated = MODE != MV_GU && MODE != MV_GU_DIRECT && !(down && GFX);
+    static_assert(!GFX || (FXS && !FUSED), "split fixed-point gate/up: FXS items, two launches");
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const size_t split_stride = (size_t)p.entries * 128;
     const int nblk128 = kts_wg >> 3;
@@ -341,7 +364,9 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         else return ld_h2(ptr);
     };
     const int nrot = m * nblk128;
-    __half2 xpre[MV_PRE], spre[MV_PRE];
+    // GFX down pass: x holds the fp16 gate rows, the up rows follow them
+    const size_t up_rows = (down && GFX) ? (size_t)p.entries * k : 0;
+    __half2 xpre[MV_PRE], spre[MV_PRE], upre[MV_PRE];
     auto preload = [&]() {
 #pragma unroll
         for (int j = 0; j < MV_PRE; ++j) {
@@ -350,6 +375,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
                 const int row = b / nblk128, bb = b - row * nblk128;
                 const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
                 xpre[j] = ld_x(x_row(row) + kg);
+                if constexpr (down && GFX) upre[j] = ld_x(x_row(row) + up_rows + kg);
                 if (!pre_rotated) spre[j] = ld_h2_ptr(suh, kg);
             }
         }
@@ -372,9 +398,10 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     //    the item (rotated here unless they arrive rotated)
     // values kk and kk + 1 of a lane sit at xs_index(kk) and xs_index(kk) + 2
     // (8-byte aligned), so (a, a, c, c) is one 64-bit LDS store
-    auto stage = [&](int b, __half2 xv, __half2 sv) {
+    auto stage = [&](int b, __half2 xv, __half2 uv, __half2 sv) {
         const int row = b / nblk128, bb = b - row * nblk128;
         const int kk = bb * 128 + 2 * lane;
+        if constexpr (down && GFX) xv = swiglu_h2(xv, uv, p.limit);
         uint32_t bits;
         if (pre_rotated) {
             bits = *reinterpret_cast<const uint32_t*>(&xv);
@@ -398,13 +425,14 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
 #pragma unroll
     for (int j = 0; j < MV_PRE; ++j) {
         const int b = wave + j * nwaves;
-        if (b < nrot) stage(b, xpre[j], spre[j]);
+        if (b < nrot) stage(b, xpre[j], (down && GFX) ? upre[j] : __half2{}, spre[j]);
     }
     for (int b = wave + MV_PRE * nwaves; b < nrot; b += nwaves) {
         const int row = b / nblk128, bb = b - row * nblk128;
         const int kg = kt_wg0 * 16 + bb * 128 + 2 * lane;
         const __half2 sv = pre_rotated ? __half2{} : ld_h2_ptr(suh, kg);
-        stage(b, ld_x(x_row(row) + kg), sv);
+        const __half2 uv = (down && GFX) ? ld_x(x_row(row) + up_rows + kg) : __half2{};
+        stage(b, ld_x(x_row(row) + kg), uv, sv);
     }
     __syncthreads();
 
@@ -419,9 +447,10 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         // epilogue vectors of this block, requested now so they are in
         // registers at the end
         const int c0 = bx * 128 + 2 * lane;
-        const __half2 ev0 = ld_h2_ptr(ev0p, c0);
+        // (GFX gate/up: only the item's own projection's svh)
+        const __half2 ev0 = ld_h2_ptr((GFX && !down && proj == 1) ? ev1p : ev0p, c0);
         __half2 ev1 = __half2{}, ev2 = __half2{};
-        if (!down) {
+        if (!down && !GFX) {
             ev1 = ld_h2_ptr(ev1p, c0);
             ev2 = ld_h2_ptr(ev2p, c0);
         }
@@ -433,7 +462,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         decode_mfma_steps<K, CB, 1, NS>(w, tiles(bx), step_stride, a_base, a_live, acc);
 
         if constexpr (FXS) {
-            static_assert(KW == 1 && (MODE == MV_DOWN || MODE == MV_DOWN_DIRECT), "split fixed-point adds: down pass");
+            static_assert(KW == 1 && (down || GFX), "split fixed-point adds: down pass, or gate/up with GFX");
             // the four waves' column slices of the unit's rows meet in LDS
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -448,6 +477,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
             // row's have been issued, so their round trips overlap
             FxPair fx{};
             int ptok = -1, pcnt = 0;
+            size_t pofs = 0;  // gate/up: the pending pair's element offset
             for (int row = wave; row < m; row += nwaves) {
                 float va = ybuf[row * 128 + 2 * lane], vb = ybuf[row * 128 + 2 * lane + 1];
                 if constexpr (CB == 2) {
@@ -458,6 +488,17 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
                 }
                 fwht128_pair_fast(va, vb, lane);
                 const int crow = crow0 + row;
+                if constexpr (!down) {
+                    // gate or up element (proj, crow, col): S contributions
+                    const size_t o = ((size_t)proj * p.entries + crow) * n + c0;
+                    const FxPair cur =
+                        fx_issue_pair(p.acc + o, (va * kHadNorm) * __low2float(ev0), (vb * kHadNorm) * __high2float(ev0));
+                    if (ptok >= 0) fx_finish_pair(fx, p.acc + pofs, S, gptr(p.out) + pofs);
+                    fx = cur;
+                    pofs = o;
+                    ptok = 0;
+                    continue;
+                }
                 const int entry = direct ? crow : uniform_i(rows_g[crow]);
                 const int t = entry / p.topk;
                 const float wv = p.weights_f16
@@ -472,8 +513,11 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
                 ptok = t;
                 pcnt = c;
             }
-            if (ptok >= 0)
+            if constexpr (!down) {
+                if (ptok >= 0) fx_finish_pair(fx, p.acc + pofs, S, gptr(p.out) + pofs);
+            } else if (ptok >= 0) {
                 fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
+            }
             continue;
         }
 
@@ -578,7 +622,6 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         };
         EXL3_GLOBAL __half* outg = gptr(p.out);
         if (!down) {
-            const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
             for (int row = wave; row < m; row += nwaves) {
                 const int crow = crow0 + row;
                 float2 gu[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
@@ -591,14 +634,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
                     h2_rn(ga * kHadNorm * __low2float(ev0), gb * kHadNorm * __high2float(ev0));
                 const __half2 uh =
                     h2_rn(ua * kHadNorm * __low2float(ev1), ub * kHadNorm * __high2float(ev1));
-                float g0 = __low2float(gh), g1 = __high2float(gh), u0 = __low2float(uh), u1 = __high2float(uh);
-                if (clamp) {
-                    g0 = fminf(g0, p.limit);
-                    g1 = fminf(g1, p.limit);
-                    u0 = fminf(fmaxf(u0, -p.limit), p.limit);
-                    u1 = fminf(fmaxf(u1, -p.limit), p.limit);
-                }
-                const __half2 act = h2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
+                const __half2 act = swiglu_h2(gh, uh, p.limit);
                 // input rotation of the down projection for this 128-wide chunk
                 const __half2 pr = __hmul2(act, ev2);
                 float da = __low2float(pr), db = __high2float(pr);
@@ -663,7 +699,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
 // workgroup b takes item r G + b for even r, r G + G - 1 - b for odd r), so
 // the workgroup with the last (lightest) item of a round takes the first
 // (heaviest) of the next.
-template <int K, int CB, int NS, int MODE, int KW, bool FXS = false>
+template <int K, int CB, int NS, int MODE, int KW, bool FXS = false, bool GFX = false>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p) {
     extern __shared__ __align__(16) unsigned char mv_smem[];
     constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
@@ -684,7 +720,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     }
     const int G = gridDim.x, b0 = blockIdx.x;
     for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0))
-        moe_item<K, CB, NS, MODE, KW, false, FXS>(p, it, mv_smem, direct_valid, rnd == 0);
+        moe_item<K, CB, NS, MODE, KW, false, FXS, GFX>(p, it, mv_smem, direct_valid, rnd == 0);
 }
 
 // One token routed directly, gate/up and down in one persistent launch.
@@ -746,7 +782,8 @@ int moe_grid_size(const void* fn, int threads, size_t smem);
 
 template <int K>
 int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
-    const bool fxs = p.fxs && p.mode == MOE_DOWN && p.kw == 1;
+    const bool gfx = p.gfx != 0;
+    const bool fxs = p.fxs && p.kw == 1 && (p.mode == MOE_DOWN || gfx);
     const size_t smem = moe_smem_bytes(4 * ns * p.kw, p.kw, fxs);
     const int threads = 256 * p.kw;
     const int mv = p.mode == MOE_DOWN ? (p.direct ? MV_DOWN_DIRECT : MV_DOWN)
@@ -754,32 +791,39 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     // a directly routed token: the item count is known here, so no
     // workgroup is launched without an item
     const int direct_items = p.topk * ((p.n >> 7) / p.bx_per_item) * p.proj_launch * p.splits;
-#define EXL3_MV_F(CBV, NSV, MVV, KWV, FXV)                                                             \
-    if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV && fxs == FXV) {                            \
-        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV, FXV>);  \
+#define EXL3_MV_G(CBV, NSV, MVV, KWV, FXV, GFV)                                                        \
+    if (cb == CBV && ns == NSV && mv == MVV && p.kw == KWV && fxs == FXV && gfx == GFV) {              \
+        const void* fn = reinterpret_cast<const void*>(&moe_gemv_kernel<K, CBV, NSV, MVV, KWV, FXV, GFV>); \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe");                                       \
         if (lrc) return lrc;                                                                           \
         int grid = moe_grid_size(fn, threads, smem);                                                   \
         if (grid <= 0) return EXL3_ERR_HIP;                                                            \
         if (p.direct && grid > direct_items) grid = direct_items;                                      \
-        moe_gemv_kernel<K, CBV, NSV, MVV, KWV, FXV><<<grid, threads, smem, st>>>(p);                   \
+        moe_gemv_kernel<K, CBV, NSV, MVV, KWV, FXV, GFV><<<grid, threads, smem, st>>>(p);              \
         return launch_status("exl3 moe launch");                                                      \
     }
+#define EXL3_MV_F(CBV, NSV, MVV, KWV, FXV) EXL3_MV_G(CBV, NSV, MVV, KWV, FXV, false)
 #define EXL3_MV_KW(CBV, NSV, MVV, KWV) EXL3_MV_F(CBV, NSV, MVV, KWV, false)
 #define EXL3_MV_NS(CBV, NSV, MVV) EXL3_MV_KW(CBV, NSV, MVV, 1) EXL3_MV_KW(CBV, NSV, MVV, 2)
 #define EXL3_MV_MODES(CBV, NSV)                                                                        \
     EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)             \
     EXL3_MV_KW(CBV, NSV, MV_GU_DIRECT, 1) EXL3_MV_KW(CBV, NSV, MV_DOWN_DIRECT, 1)                        \
     EXL3_MV_F(CBV, NSV, MV_DOWN, 1, true) EXL3_MV_F(CBV, NSV, MV_DOWN_DIRECT, 1, true)
-#define EXL3_MV_CASE(CBV) \
-    EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 12) EXL3_MV_MODES(CBV, 16)
+#define EXL3_MV_GFX(CBV, NSV) \
+    EXL3_MV_G(CBV, NSV, MV_GU_DIRECT, 1, true, true) EXL3_MV_G(CBV, NSV, MV_DOWN_DIRECT, 1, true, true)
+#define EXL3_MV_CASE(CBV)                                                                                     \
+    EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 12) EXL3_MV_MODES(CBV, 16) \
+    EXL3_MV_GFX(CBV, 2) EXL3_MV_GFX(CBV, 4) EXL3_MV_GFX(CBV, 8)
     EXL3_MV_CASE(0) EXL3_MV_CASE(1) EXL3_MV_CASE(2)
 #undef EXL3_MV_CASE
 #undef EXL3_MV_MODES
+#undef EXL3_MV_GFX
 #undef EXL3_MV_NS
 #undef EXL3_MV_KW
 #undef EXL3_MV_F
-    set_error("exl3 moe: no kernel for codebook %d steps %d k waves %d", cb, ns, p.kw);
+#undef EXL3_MV_G
+    set_error("exl3 moe: no kernel for codebook %d steps %d k waves %d%s", cb, ns, p.kw,
+              gfx ? " (split fixed-point gate/up)" : "");
     return EXL3_ERR_UNSUPPORTED;
 }
 
@@ -787,6 +831,9 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
 // smaller of moe_grid_size's estimate and the runtime's occupancy figure
 // (the fused launch relies on every workgroup being resident).
 int moe_fused_grid_size(const void* fn, size_t smem);
+
+// Step counts of the split fixed-point gate/up instances (and their down pass).
+inline bool moe_gfx_steps_ok(int ns) { return ns == 2 || ns == 4 || ns == 8; }
 
 // Step counts the fused one-token kernel is instantiated for (per pass).
 inline bool moe_fused_steps_ok(int ns) { return ns == 2 || ns == 4 || ns == 8; }

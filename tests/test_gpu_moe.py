@@ -346,6 +346,81 @@ def test_moe_one_token_fused_graph(monkeypatch):
     check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe fused graph new routing")
 
 
+@pytest.mark.parametrize("E,hidden,inter,Ks,cb,topk,invalid,gu_ns,limit", [
+    (16, 256, 384, (3, 3, 3), 1, 8, 0, 4, 0.0),
+    (8, 512, 256, (2, 2, 2), 2, 6, 2, 2, 0.0),       # mul1: per-split row sums in the fixed-point adds
+    (8, 256, 768, (4, 4, 4), 0, 4, 1, 4, 0.0),       # 3INST
+    (8, 256, 256, (3, 3, 3), 1, 4, 4, 4, 0.0),       # no valid slot: zero row
+    (128, 2048, 768, (3, 3, 3), 1, 8, 0, 4, 0.0),    # headline MoE shape
+    (128, 2048, 768, (3, 3, 3), 1, 8, 0, 2, 0.0),    # 16 splits
+    (32, 1024, 1536, (5, 5, 5), 2, 8, 3, 8, 0.0),
+    (8, 512, 384, (3, 4, 2), 1, 4, 0, 4, 0.0),       # gate != up: two gate/up launches
+    (8, 256, 256, (4, 4, 4), 1, 4, 0, 4, 2.0),       # SwiGLU clamp in the down staging
+])
+def test_moe_one_token_split_fixed_point_gate_up(E, hidden, inter, Ks, cb, topk, invalid, gu_ns, limit, monkeypatch):
+    """One token, two launches (EXL3_MOE_GFX, default on): gate/up items add their rotated, scaled
+    partial rows into fixed-point accumulators, each element's completing add writes the fp16 gate
+    or up value, and the down pass stages the SwiGLU from them.  Against the oracle, against the
+    partial-row hand-off (EXL3_MOE_GFX=0) within the same bar, repeated calls bit-identical (the
+    accumulators are left clear), skipped slots and a token without valid slots."""
+    print(f"case: moe gfx one token E={E} h={hidden} i={inter} K={Ks} cb={cb} topk={topk} invalid={invalid} "
+          f"gu_ns={gu_ns} limit={limit}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_GFX_GU_NSTEPS", str(gu_ns))
+    ex = Experts(E, hidden, inter, Ks, cb, seed=190 + E + Ks[0])
+    x = make_x(1, hidden, seed=191 + Ks[0])
+    ids, w = _routing(1, topk, E, seed=192 + invalid)
+    ids[0, :invalid] = [-1 if j % 2 else E + j for j in range(invalid)]
+    monkeypatch.setenv("EXL3_MOE_GFX", "0")
+    base = _layer_capi(ex, x, ids, w, cb=cb, limit=limit)
+    monkeypatch.setenv("EXL3_MOE_GFX", "1")
+    a = _layer_capi(ex, x, ids, w, cb=cb, limit=limit)
+    b = _layer_capi(ex, x, ids, w, cb=cb, limit=limit)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "repeated call differs"
+    o = a.float().cpu().numpy()
+    if invalid == topk:
+        assert np.all(o == 0.0)
+        return
+    ref = ex.ref(x, ids, w, limit if limit > 0 else float("inf"))
+    check_close(o, ref, f"moe gfx one token E={E}")
+    check_close(o, base.float().cpu().numpy(), f"moe gfx vs partial-row hand-off E={E}")
+
+
+def test_moe_one_token_split_fixed_point_graph():
+    """The split fixed-point gate/up path captured in a HIP graph: replays interleaved with eager
+    calls match the eager result, and a routing change between replays is picked up."""
+    E, hidden, inter, topk = 32, 512, 768, 8
+    ex = Experts(E, hidden, inter, (3, 3, 3), 1, seed=195)
+    x = make_x(1, hidden, seed=196)
+    ids, w = _routing(1, topk, E, seed=197)
+    xd, idd, wd = (torch.from_numpy(a).cuda() for a in (x, ids, w))
+    a = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gout = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, a), f"graph replay {r} differs from eager"
+        ex.layer(xd, idd, wd)
+        torch.cuda.synchronize()
+    ids2, w2 = _routing(1, topk, E, seed=198)
+    ids2[0, 5] = E + 1
+    idd.copy_(torch.from_numpy(ids2))
+    wd.copy_(torch.from_numpy(w2))
+    g.replay()
+    torch.cuda.synchronize()
+    check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe gfx graph new routing")
+
+
 @pytest.mark.parametrize("T,topk,E,hidden,inter,K,cb,invalid", [
     (1, 8, 16, 256, 768, 3, 1, 0), (1, 6, 8, 512, 384, 4, 2, 2), (5, 4, 8, 256, 1536, 3, 0, 3),
     (16, 8, 32, 512, 768, 2, 1, 4), (12, 2, 4, 256, 256, 5, 2, 0),
