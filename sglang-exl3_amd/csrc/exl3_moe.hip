@@ -406,6 +406,7 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
 // 109.0 -> 106.0 us; K = 4: 119.2 -> 115.1 us).
 constexpr int kMoeRotTokens = 2;
 constexpr int kMoeFusedCombineTokens = 16;
+constexpr int kMoeGfxTokens = 3;  // routed batches with the split fixed-point gate/up pass
 
 struct MoeLayout {
     int entries, max_units;
@@ -445,10 +446,10 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     // Env EXL3_MOE_FC_TOKENS overrides the threshold (0: never fused).
     const int fc_tokens = env_int("EXL3_MOE_FC_TOKENS", kMoeFusedCombineTokens);
     L.fc = tokens <= fc_tokens && (size_t)tokens * hidden * 8 <= kWsAccBytes && topk <= SK_MAX_CONTRIB;
-    // h: the rotated activation rows; one token: room for the fp16 gate and up
-    // rows of the split fixed-point gate/up pass instead
+    // h: the rotated activation rows; with the fused combine, room for the
+    // fp16 gate and up rows of the split fixed-point gate/up pass instead
     L.h_off = o;
-    o = align256(o + (size_t)(tokens == 1 ? 2 : 1) * L.entries * inter * 2);
+    o = align256(o + (size_t)(L.fc ? 2 : 1) * L.entries * inter * 2);
     L.y_off = o;
     o = align256(o + (size_t)L.entries * hidden * 2);
     L.rot = tokens >= env_int("EXL3_MOE_ROT_TOKENS", kMoeRotTokens);
@@ -553,15 +554,22 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     // partial rows into the output accumulators) when every token's count of
     // contributions (valid slots x splits) fits the accumulators' count bits
     const bool dn_fxs = L.fc && L.dn.kw == 1 && topk * L.dn.splits <= SK_MAX_CONTRIB && env_int("EXL3_MOE_FXS", 1) != 0;
-    // One token in two launches: gate/up by split fixed-point adds (no
-    // partial rows, counter or last arrival; each element's completing add
-    // writes the fp16 gate or up value), and the down pass stages the SwiGLU
-    // from those rows, rotated with its own suh.  The split hand-off being one
-    // round trip, the gate/up items are cut finer (env EXL3_MOE_GFX_GU_NSTEPS,
-    // default 4 steps).  Env EXL3_MOE_GFX=0 keeps the partial-row hand-off.
+    // Gate/up by split fixed-point adds (no partial rows, counter or last
+    // arrival; each element's completing add writes the fp16 gate or up
+    // value), and the down pass stages the SwiGLU from those rows, rotated with
+    // its own suh.  The split hand-off being one round trip, the gate/up items
+    // are cut finer for one token (env EXL3_MOE_GFX_GU_NSTEPS; default 4 steps
+    // there, the planner's otherwise).  One token (direct) or rotated routed
+    // batches up to kMoeGfxTokens (env EXL3_MOE_GFX_TOKENS; EXL3_MOE_GFX=0
+    // keeps the partial-row hand-off).  Graph-timed on config 4, partial rows
+    // -> split fixed-point: B = 1 / 2 / 3: 19.0 / 24.2 / 25.8 -> 16.8 / 22.6 /
+    // 24.1 us; B = 4 / 6: 27.9 / 29.9 -> 28.8 / 31.1; B = 8 / 12: 38.9 / 43.2
+    // -> 37.0 / 41.7; B = 16: 47.1 -> 49.2 (16-row units: every down item
+    // then rotates up to 16 SwiGLU rows per k block, and the adds contend).
     const int gu_kslices = hidden / 16;
-    const int gfx_ns = env_int("EXL3_MOE_GFX_GU_NSTEPS", 4);
-    const bool gfx = direct && !fused && dn_fxs && moe_gfx_steps_ok(gfx_ns) && moe_gfx_steps_ok(L.dn.ns) &&
+    const int gfx_ns = env_int("EXL3_MOE_GFX_GU_NSTEPS", direct ? 4 : L.gu.ns);
+    const bool gfx = (direct || (L.rot && tokens <= env_int("EXL3_MOE_GFX_TOKENS", kMoeGfxTokens))) && !fused &&
+                     dn_fxs && moe_gfx_steps_ok(gfx_ns) && moe_gfx_steps_ok(L.dn.ns) &&
                      gu_kslices % (4 * gfx_ns) == 0 && gu_kslices / (4 * gfx_ns) <= SK_MAX_CONTRIB &&
                      ((size_t)tokens * hidden + (size_t)2 * L.entries * inter) * 8 <= kWsAccBytes &&
                      env_int("EXL3_MOE_GFX", 1) != 0;

@@ -809,8 +809,9 @@ int moe_launch_k(int cb, int ns, const MoeParams& p, hipStream_t st) {
     EXL3_MV_NS(CBV, NSV, MV_GU) EXL3_MV_NS(CBV, NSV, MV_GU_ROT) EXL3_MV_NS(CBV, NSV, MV_DOWN)             \
     EXL3_MV_KW(CBV, NSV, MV_GU_DIRECT, 1) EXL3_MV_KW(CBV, NSV, MV_DOWN_DIRECT, 1)                        \
     EXL3_MV_F(CBV, NSV, MV_DOWN, 1, true) EXL3_MV_F(CBV, NSV, MV_DOWN_DIRECT, 1, true)
-#define EXL3_MV_GFX(CBV, NSV) \
-    EXL3_MV_G(CBV, NSV, MV_GU_DIRECT, 1, true, true) EXL3_MV_G(CBV, NSV, MV_DOWN_DIRECT, 1, true, true)
+#define EXL3_MV_GFX(CBV, NSV)                                                                             \
+    EXL3_MV_G(CBV, NSV, MV_GU_DIRECT, 1, true, true) EXL3_MV_G(CBV, NSV, MV_DOWN_DIRECT, 1, true, true)      \
+    EXL3_MV_G(CBV, NSV, MV_GU_ROT, 1, true, true) EXL3_MV_G(CBV, NSV, MV_DOWN, 1, true, true)
 #define EXL3_MV_CASE(CBV)                                                                                     \
     EXL3_MV_MODES(CBV, 2) EXL3_MV_MODES(CBV, 4) EXL3_MV_MODES(CBV, 8) EXL3_MV_MODES(CBV, 12) EXL3_MV_MODES(CBV, 16) \
     EXL3_MV_GFX(CBV, 2) EXL3_MV_GFX(CBV, 4) EXL3_MV_GFX(CBV, 8)

@@ -386,6 +386,40 @@ def test_moe_one_token_split_fixed_point_gate_up(E, hidden, inter, Ks, cb, topk,
     check_close(o, base.float().cpu().numpy(), f"moe gfx vs partial-row hand-off E={E}")
 
 
+@pytest.mark.parametrize("T,topk,E,hidden,inter,Ks,cb,invalid,gu_ns", [
+    (2, 8, 16, 256, 384, (3, 3, 3), 1, 0, 4),
+    (5, 4, 8, 512, 256, (2, 2, 2), 2, 3, 8),
+    (16, 8, 32, 512, 768, (3, 3, 3), 1, 4, 4),
+    (16, 8, 128, 2048, 768, (3, 3, 3), 1, 0, 4),    # headline MoE shape
+    (9, 6, 8, 256, 256, (4, 3, 2), 0, 2, 2),        # 3INST, gate != up
+])
+def test_moe_batch_split_fixed_point_gate_up(T, topk, E, hidden, inter, Ks, cb, invalid, gu_ns, monkeypatch):
+    """Routed batches with the fused combine: the split fixed-point gate/up pass on the rotated rows
+    (EXL3_MOE_GFX) against the oracle and the partial-row hand-off, repeated calls bit-identical, a
+    token without valid slots a zero row."""
+    print(f"case: moe gfx batch T={T} topk={topk} E={E} h={hidden} i={inter} K={Ks} cb={cb} gu_ns={gu_ns}",
+          flush=True)
+    monkeypatch.setenv("EXL3_MOE_GFX_GU_NSTEPS", str(gu_ns))
+    monkeypatch.setenv("EXL3_MOE_GFX_TOKENS", "16")  # above the default threshold too
+    ex = Experts(E, hidden, inter, Ks, cb, seed=200 + T + E)
+    x = make_x(T, hidden, seed=201 + T)
+    ids, w = _routing(T, topk, E, seed=202 + T, invalid=invalid)
+    if T > 2:
+        ids[T // 2, :] = -1
+    monkeypatch.setenv("EXL3_MOE_GFX", "0")
+    base = _layer_capi(ex, x, ids, w, cb=cb)
+    monkeypatch.setenv("EXL3_MOE_GFX", "1")
+    a = _layer_capi(ex, x, ids, w, cb=cb)
+    b = _layer_capi(ex, x, ids, w, cb=cb)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "repeated call differs"
+    o = a.float().cpu().numpy()
+    if T > 2:
+        assert np.all(o[T // 2] == 0.0)
+    check_close(o, ex.ref(x, ids, w), f"moe gfx batch T={T}")
+    check_close(o, base.float().cpu().numpy(), f"moe gfx batch vs partial-row hand-off T={T}")
+
+
 def test_moe_one_token_split_fixed_point_graph():
     """The split fixed-point gate/up path captured in a HIP graph: replays interleaved with eager
     calls match the eager result, and a routing change between replays is picked up."""
