@@ -208,6 +208,9 @@ __device__ __forceinline__ FxPair fx_issue_pair(unsigned long long* acc, float a
 // two fp16 values go out as one 4-byte store.  Storing the first element
 // before reading the second had the wave wait for that store's round trip
 // too (config 2 m = 1: 10.97 -> 10.64 us).
+// COH: device-coherent stores, for outputs that other workgroups of the same
+// launch read.
+template <bool COH = false>
 __device__ __forceinline__ void fx_finish_pair(const FxPair& f, unsigned long long* acc, int cnt,
                                                EXL3_GLOBAL __half* y) {
     const bool ca = (int)(f.oa >> SK_CNT_SHIFT) == cnt - 1;
@@ -215,11 +218,19 @@ __device__ __forceinline__ void fx_finish_pair(const FxPair& f, unsigned long lo
     if (!(ca || cb)) return;
     const float va = sk_decode(f.oa + f.ea, cnt), vb = sk_decode(f.ob + f.eb, cnt);
     if (ca && cb) {
-        st_h2(y, __floats2half2_rn(va, vb));
-    } else if (ca) {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y) = __half_as_ushort(__float2half_rn(va));
+        const __half2 v = __floats2half2_rn(va, vb);
+        if constexpr (COH)
+            __hip_atomic_store(reinterpret_cast<uint32_t*>((__half*)y), *reinterpret_cast<const uint32_t*>(&v),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            st_h2(y, v);
     } else {
-        *reinterpret_cast<EXL3_GLOBAL uint16_t*>(y + 1) = __half_as_ushort(__float2half_rn(vb));
+        EXL3_GLOBAL uint16_t* const d = reinterpret_cast<EXL3_GLOBAL uint16_t*>(ca ? y : y + 1);
+        const uint16_t h = __half_as_ushort(__float2half_rn(ca ? va : vb));
+        if constexpr (COH)
+            __hip_atomic_store((uint16_t*)d, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            *d = h;
     }
     if (ca) __hip_atomic_store(acc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (cb) __hip_atomic_store(acc + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

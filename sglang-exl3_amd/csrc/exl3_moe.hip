@@ -545,10 +545,10 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     // stay off the lines of other units' flags and of the hand-off counters
     int ready_stride = env_int("EXL3_MOE_READY_STRIDE", 256);
     if (ready_stride < inter / 128) ready_stride = inter / 128;
-    const bool fused = direct && KG == KU && KU == KD && moe_fused_steps_ok(L.gu.ns) && moe_fused_steps_ok(L.dn.ns) &&
-                       L.gu.kw == 1 && L.dn.kw == 1 &&
-                       (size_t)topk * (inter / 128 + hidden / 128 + ready_stride + 1) + 258 <= kWsMaxCounters &&
-                       env_int("EXL3_MOE_FUSED", 0) != 0;
+    const bool fuse_req = direct && KG == KU && KU == KD && L.gu.kw == 1 && L.dn.kw == 1 &&
+                          moe_fused_steps_ok(L.dn.ns) &&
+                          (size_t)topk * (inter / 128 + hidden / 128 + ready_stride + 1) + 258 <= kWsMaxCounters &&
+                          env_int("EXL3_MOE_FUSED", 0) != 0;
 
     // the fused combine one round trip per split (each split adds its rotated
     // partial rows into the output accumulators) when every token's count of
@@ -567,13 +567,14 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     // -> 37.0 / 41.7; B = 16: 47.1 -> 49.2 (16-row units: every down item
     // then rotates up to 16 SwiGLU rows per k block, and the adds contend).
     const int gu_kslices = hidden / 16;
-    const int gfx_ns = env_int("EXL3_MOE_GFX_GU_NSTEPS", direct ? 4 : L.gu.ns);
-    const bool gfx = (direct || (L.rot && tokens <= env_int("EXL3_MOE_GFX_TOKENS", kMoeGfxTokens))) && !fused &&
+    const int gfx_ns = env_int("EXL3_MOE_GFX_GU_NSTEPS", direct ? (fuse_req ? 8 : 4) : L.gu.ns);
+    const bool gfx = (direct || (L.rot && tokens <= env_int("EXL3_MOE_GFX_TOKENS", kMoeGfxTokens))) &&
                      dn_fxs && moe_gfx_steps_ok(gfx_ns) && moe_gfx_steps_ok(L.dn.ns) &&
                      gu_kslices % (4 * gfx_ns) == 0 && gu_kslices / (4 * gfx_ns) <= SK_MAX_CONTRIB &&
                      ((size_t)tokens * hidden + (size_t)2 * L.entries * inter) * 8 <= kWsAccBytes &&
                      env_int("EXL3_MOE_GFX", 1) != 0;
     const int gu_ns = gfx ? gfx_ns : L.gu.ns;
+    const bool fused = fuse_req && moe_fused_steps_ok(gu_ns);
     unsigned long long* const acc_base = reinterpret_cast<unsigned long long*>(w8 + kWsAccOffset);
 
     // 3. gate + up (+ SwiGLU + down input rotation; GFX: the gate and up rows)
@@ -606,6 +607,7 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
         pg.status = c0 + kWsStatusIndex;
         pg.ready_nblk = nbg;
         pg.ready_stride = ready_stride;
+        pg.ready_target = gfx ? 2 * pg.splits : 1;
         pg.poll_sleep = env_int("EXL3_MOE_POLL_SLEEP", 1);
         pg.prime_late = env_int("EXL3_MOE_PRIME_LATE", 0);
     } else if (KG == KU) {
@@ -650,13 +652,15 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
         p.done = pg.done;
         p.ready_nblk = pg.ready_nblk;
         p.ready_stride = pg.ready_stride;
+        p.ready_target = pg.ready_target;
         p.poll_sleep = pg.poll_sleep;
         p.prime_late = pg.prime_late;
         p.max_polls = pg.max_polls;
         p.status = pg.status;
         p.ticket = pg.ticket;
         p.dn_items_per_unit = ((hidden / 128) / L.dn.bpi) * L.dn.splits;
-        rc = moe_fused_launch(KD, cb, L.gu.ns, L.dn.ns, pg, p, st);
+        p.gfx = gfx;
+        rc = moe_fused_launch(KD, cb, gu_ns, L.dn.ns, pg, p, st);
     } else {
         rc = moe_launch(KD, cb, L.dn.ns, p, st);
     }

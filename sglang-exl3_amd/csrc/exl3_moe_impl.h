@@ -120,6 +120,7 @@ struct MoeParams {
     int poll_sleep;    // s_sleep(8) calls between two polls
     int prime_late;    // down items request their weights after the wait
     int dn_items_per_unit;
+    int ready_target;  // count that marks an h block ready: 1, or 2 S (split fixed-point gate/up)
     // Down pass with the fused combine, one round trip per split (fxs != 0,
     // moe_gemv_kernel<.., FXS = true>): each k-split item rotates and scales
     // its own partial rows and adds w * svh * H(partial) / sqrt(128) straight
@@ -190,15 +191,15 @@ __device__ __forceinline__ __half2 swiglu_h2(__half2 g, __half2 u, float limit) 
     return h2_rn(silu_f(g0) * u0, silu_f(g1) * u1);
 }
 
-// Wait until the readiness flags f[j0..j1] are all set (one thread), for at
-// most max_polls polls (each followed by nsleep s_sleep(8) calls, ~0.2 us
-// each): a bound so that every wave exits even if a producer never ran.
+// Wait until the readiness counts f[j0..j1] all reach `target` (one thread),
+// for at most max_polls polls (each followed by nsleep s_sleep(8) calls, ~0.2
+// us each): a bound so that every wave exits even if a producer never ran.
 // Returns false when the wait gave up.
-__device__ __forceinline__ bool wait_ready(const int* f, int j0, int j1, int nsleep, int max_polls) {
+__device__ __forceinline__ bool wait_ready(const int* f, int j0, int j1, int target, int nsleep, int max_polls) {
     for (int it = 0; it < max_polls; ++it) {
         bool ok = true;
         for (int j = j0; j <= j1; ++j)
-            ok = ok && __hip_atomic_load(const_cast<int*>(f) + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+            ok = ok && __hip_atomic_load(const_cast<int*>(f) + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
         if (ok) return true;
         for (int z = 0; z < nsleep; ++z) __builtin_amdgcn_s_sleep(8);
     }
@@ -277,7 +278,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     constexpr bool down = MODE == MV_DOWN || MODE == MV_DOWN_DIRECT;
     // input rows arrive rotated (a GFX down pass rotates the SwiGLU it stages)
     constexpr bool pre_rotated = MODE != MV_GU && MODE != MV_GU_DIRECT && !(down && GFX);
-    static_assert(!GFX || (FXS && !FUSED), "split fixed-point gate/up: FXS items, two launches");
+    static_assert(!GFX || FXS, "split fixed-point gate/up: FXS items");
     const size_t step_stride = (size_t)4 * ntiles * (8 * K);
     const size_t split_stride = (size_t)p.entries * 128;
     const int nblk128 = kts_wg >> 3;
@@ -384,7 +385,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     if constexpr (wait_h) {
         if (!p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
         if (tid == 0 && !wait_ready(p.ready + (size_t)u * p.ready_stride, kt_wg0 >> 3, (kt_wg0 + kts_wg - 1) >> 3,
-                                    p.poll_sleep, p.max_polls))
+                                    p.ready_target, p.poll_sleep, p.max_polls))
             report_wait_expired(p.status, EXL3_WAIT_MOE_FUSED);
         __syncthreads();
         if (p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
@@ -435,6 +436,18 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         stage(b, ld_x(x_row(row) + kg), uv, sv);
     }
     __syncthreads();
+    if constexpr (wait_h && FXS) {
+        // a fused down item with split fixed-point adds has read its h rows:
+        // count it done; the unit's last down item clears the unit's
+        // readiness counts for the next call
+        if (tid == 0 && __hip_atomic_fetch_add(p.done + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                            p.dn_items_per_unit - 1) {
+            for (int j = 0; j < p.ready_nblk; ++j)
+                __hip_atomic_store(p.ready + (size_t)u * p.ready_stride + j, 0, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.done + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 
     const bool live = i < m;
     const _Float16* a_base[1] = {xs + (size_t)((live ? i : 0) * kts_wg + kwi * 4 * nsteps + g) * 4 * 8};
@@ -493,7 +506,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
                     const size_t o = ((size_t)proj * p.entries + crow) * n + c0;
                     const FxPair cur =
                         fx_issue_pair(p.acc + o, (va * kHadNorm) * __low2float(ev0), (vb * kHadNorm) * __high2float(ev0));
-                    if (ptok >= 0) fx_finish_pair(fx, p.acc + pofs, S, gptr(p.out) + pofs);
+                    if (ptok >= 0) fx_finish_pair<FUSED>(fx, p.acc + pofs, S, gptr(p.out) + pofs);
                     fx = cur;
                     pofs = o;
                     ptok = 0;
@@ -514,7 +527,17 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
                 pcnt = c;
             }
             if constexpr (!down) {
-                if (ptok >= 0) fx_finish_pair(fx, p.acc + pofs, S, gptr(p.out) + pofs);
+                if (ptok >= 0) fx_finish_pair<FUSED>(fx, p.acc + pofs, S, gptr(p.out) + pofs);
+                if constexpr (FUSED) {
+                    // this item's share of the block's gate or up elements is
+                    // in (and the elements it completed are stored): count it
+                    // toward the block's 2 S
+                    wait_stores();
+                    __syncthreads();
+                    if (tid == 0)
+                        __hip_atomic_fetch_add(p.ready + (size_t)u * p.ready_stride + bx, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                }
             } else if (ptok >= 0) {
                 fx_finish_pair(fx, p.acc + (size_t)ptok * n + c0, pcnt, gptr(p.final_out) + (size_t)ptok * n + c0);
             }
@@ -738,7 +761,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
 // them from being resident, the wait gives up and sets EXL3_WAIT_MOE_FUSED in
 // the workspace status word.  (Claiming every item from the ticket measured
 // 38.4 against 22 us on config 4 B = 1: 768 contended atomics on one word.)
-template <int K, int CB, int NSG, int NSD>
+template <int K, int CB, int NSG, int NSD, bool GFX = false>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(MoeParams pg, MoeParams pd) {
     extern __shared__ __align__(16) unsigned char mv_smem[];
     __shared__ int claimed;
@@ -751,8 +774,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
     const int total = ngu + pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
     const int G = gridDim.x;
     for (int rnd = 0, it = blockIdx.x; it < total; ++rnd) {
-        if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true>(pg, it, mv_smem, direct_valid, rnd == 0);
-        else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true>(pd, it - ngu, mv_smem, direct_valid, rnd == 0);
+        if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true, GFX, GFX>(pg, it, mv_smem, direct_valid, rnd == 0);
+        else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true, GFX, GFX>(pd, it - ngu, mv_smem, direct_valid, rnd == 0);
         if (G >= total) break;
         __syncthreads();
         if (threadIdx.x == 0)
@@ -841,22 +864,25 @@ inline bool moe_fused_steps_ok(int ns) { return ns == 2 || ns == 4 || ns == 8; }
 
 template <int K>
 int moe_fused_launch_k(int cb, int nsg, int nsd, const MoeParams& pg, const MoeParams& pd, hipStream_t st) {
-    const size_t sg = moe_smem_bytes(4 * nsg, 1), sd = moe_smem_bytes(4 * nsd, 1);
+    const bool gfx = pg.gfx != 0;
+    const size_t sg = moe_smem_bytes(4 * nsg, 1, gfx), sd = moe_smem_bytes(4 * nsd, 1, gfx);
     const size_t smem = sg > sd ? sg : sd;
     const int items = pg.topk * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits +
                       pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
-#define EXL3_MF(CBV, NG, ND)                                                                           \
-    if (cb == CBV && nsg == NG && nsd == ND) {                                                         \
-        const void* fn = reinterpret_cast<const void*>(&moe_fused_direct_kernel<K, CBV, NG, ND>);      \
+#define EXL3_MF(CBV, NG, ND, GFV)                                                                      \
+    if (cb == CBV && nsg == NG && nsd == ND && gfx == GFV) {                                           \
+        const void* fn = reinterpret_cast<const void*>(&moe_fused_direct_kernel<K, CBV, NG, ND, GFV>); \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe fused");                                 \
         if (lrc) return lrc;                                                                           \
         int grid = moe_fused_grid_size(fn, smem);                                                      \
         if (grid <= 0) return EXL3_ERR_HIP;                                                            \
         if (grid > items) grid = items;                                                                \
-        moe_fused_direct_kernel<K, CBV, NG, ND><<<grid, 256, smem, st>>>(pg, pd);                      \
+        moe_fused_direct_kernel<K, CBV, NG, ND, GFV><<<grid, 256, smem, st>>>(pg, pd);                 \
         return launch_status("exl3 moe fused launch");                                                 \
     }
-#define EXL3_MF_G(CBV, NG) EXL3_MF(CBV, NG, 2) EXL3_MF(CBV, NG, 4) EXL3_MF(CBV, NG, 8)
+#define EXL3_MF_G(CBV, NG)                                                                                    \
+    EXL3_MF(CBV, NG, 2, false) EXL3_MF(CBV, NG, 4, false) EXL3_MF(CBV, NG, 8, false) EXL3_MF(CBV, NG, 2, true) \
+    EXL3_MF(CBV, NG, 4, true) EXL3_MF(CBV, NG, 8, true)
 #define EXL3_MF_CB(CBV) EXL3_MF_G(CBV, 2) EXL3_MF_G(CBV, 4) EXL3_MF_G(CBV, 8)
     EXL3_MF_CB(0) EXL3_MF_CB(1) EXL3_MF_CB(2)
 #undef EXL3_MF_CB

@@ -310,6 +310,42 @@ def test_moe_one_token_fused_launch(E, hidden, inter, K, cb, topk, invalid, fc_t
         check_close(o, ex.ref(x, ids, w), f"moe fused one token E={E}")
 
 
+@pytest.mark.parametrize("E,hidden,inter,K,cb,topk,invalid,gu_ns", [
+    (16, 256, 384, 3, 1, 8, 0, 4),
+    (8, 512, 256, 2, 2, 6, 2, 8),
+    (8, 256, 768, 4, 0, 4, 1, 2),
+    (8, 256, 256, 3, 1, 4, 4, 4),        # no valid slot: zero row
+    (128, 2048, 768, 3, 1, 8, 0, 8),     # headline MoE shape
+    (32, 1024, 1536, 5, 2, 8, 3, 8),
+])
+def test_moe_one_token_fused_split_fixed_point(E, hidden, inter, K, cb, topk, invalid, gu_ns, monkeypatch):
+    """One token in one launch with the split fixed-point gate/up (EXL3_MOE_FUSED=1, EXL3_MOE_GFX
+    on): down items wait until the 2 S gate/up items of each h block have added (and stored the
+    elements they completed).  Same bits as the two launches with the same gate/up items, repeated
+    calls agree (readiness counts and accumulators are left clear), and against the oracle."""
+    print(f"case: moe fused gfx one token E={E} h={hidden} i={inter} K={K} cb={cb} topk={topk} invalid={invalid} "
+          f"gu_ns={gu_ns}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_GFX_GU_NSTEPS", str(gu_ns))
+    ex = Experts(E, hidden, inter, (K, K, K), cb, seed=210 + E + K)
+    x = make_x(1, hidden, seed=211 + K)
+    ids, w = _routing(1, topk, E, seed=212 + invalid)
+    ids[0, :invalid] = [-1 if j % 2 else E + j for j in range(invalid)]
+    outs = {}
+    for fused in ("0", "1", "1"):
+        monkeypatch.setenv("EXL3_MOE_FUSED", fused)
+        o = _layer_capi(ex, x, ids, w, cb=cb)
+        torch.cuda.synchronize()
+        if fused in outs:
+            assert torch.equal(o, outs[fused]), "repeated fused call differs"
+        outs[fused] = o
+    assert torch.equal(outs["0"], outs["1"]), "fused launch differs from the two launches"
+    o = outs["1"].float().cpu().numpy()
+    if invalid == topk:
+        assert np.all(o == 0.0)
+    else:
+        check_close(o, ex.ref(x, ids, w), f"moe fused gfx one token E={E}")
+
+
 def test_moe_one_token_fused_graph(monkeypatch):
     """The fused one-token launch captured in a HIP graph: replays interleaved with eager calls
     match the eager result, and a routing change between replays is picked up."""
