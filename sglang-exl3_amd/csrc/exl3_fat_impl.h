@@ -27,8 +27,10 @@
 namespace exl3 {
 
 // Wave priority 1 over the MFMA phase of the wide-tile kernel, so the matrix
-// core is fed first while the co-resident workgroup decodes (config 3, M=2048:
-// 552 -> 545 us).  Build with -DEXL3_FAT_SETPRIO=0 to leave priorities alone.
+// core is fed first while the SIMD's other wave decodes (config 3, M=2048:
+// 552 -> 545 us before the ping-pong schedule; with it, priority 0 or raising
+// the decoding wave instead measured 537 / 535 against 528 us).  Build with
+// -DEXL3_FAT_SETPRIO=0 to leave priorities alone.
 #ifndef EXL3_FAT_SETPRIO
 #define EXL3_FAT_SETPRIO 1
 #endif
@@ -421,10 +423,12 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
 // chunk-major ([quarter][group][chunk][lane] x 16 bytes), so their 16-byte
 // writes and reads are conflict-free too.
 //
-// Step s: decode this wave's group of step s+1 into the other B buffer,
-// request the weights of step s+2 and the A chunks of step s+1, run the
-// step's 64 MFMAs on the current buffers, write the A chunks; one barrier per
-// step, which waits for the LDS traffic only.
+// Step s: request the A chunks of step s+1; phase A: the row-half-0 waves
+// run the step's 64 MFMAs on the current buffers while the row-half-1 waves
+// decode their group of step s+1 into the other B buffer and request the
+// weights of step s+2; phase B: the same with the roles swapped; then the A
+// chunks are written.  Two barriers per step, which wait for the LDS traffic
+// only.
 constexpr int FB_ROWS = 256;
 constexpr int FB_COLS = 256;
 constexpr int FB_THREADS = 512;                 // 8 waves: 2 row halves x 4 column quarters
@@ -610,23 +614,46 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
             }
         }
     };
-    // The decode and MFMA phases are kept apart (sched_barrier): mixing them
-    // raises register pressure past the 256 of two waves per SIMD.
+    // Ping-pong: each step has two phases, one barrier after each.  In phase A
+    // the row-half-0 waves run the step's MFMAs while the row-half-1 waves
+    // decode their group of step s+1; in phase B the roles swap.  The two
+    // waves of a SIMD (the same column quarter) are then never in the same
+    // role, so one's decode and the other's MFMAs share the SIMD instead of
+    // both waves decoding, then both multiplying (config 3 M=2048, graph-timed
+    // on one box: 547 -> 528 us).  A chunks of step s+1 are requested at the
+    // start of step s and written after phase B; the B buffer a phase writes
+    // was last read in the step before (both phases).  Decode and MFMA code
+    // are kept apart (sched_barrier): mixing them raises register pressure
+    // past the 256 of two waves per SIMD.
+    auto run_mfma = [&](auto slot_c) {
+        if constexpr (EXL3_FAT_SETPRIO) __builtin_amdgcn_s_setprio(1);
+        mfma_phase(slot_c);
+        if constexpr (EXL3_FAT_SETPRIO) __builtin_amdgcn_s_setprio(0);
+    };
     auto step_body = [&](int s, auto slot_c) {
         constexpr int SL = decltype(slot_c)::value;
         const int n1 = s + 1 < nsteps ? s + 1 : s;
         const int n2 = s + 2 < nsteps ? s + 2 : n1;
-        decode_post(SL ^ 1);
-        load_step(n2);
         load_a(n1);
+        if (rh == 0) {  // phase A
+            run_mfma(slot_c);
+        } else {
+            decode_post(SL ^ 1);
+            load_step(n2);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (EXL3_FAT_SETPRIO) __builtin_amdgcn_s_setprio(1);
-        mfma_phase(slot_c);
-        if constexpr (EXL3_FAT_SETPRIO) __builtin_amdgcn_s_setprio(0);
-        __builtin_amdgcn_sched_barrier(0);
-        write_a(SL ^ 1);
         // A barrier on the LDS traffic only (__syncthreads would also wait for
         // the weight request, which the next decode waits for by itself).
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (rh != 0) {  // phase B
+            run_mfma(slot_c);
+        } else {
+            decode_post(SL ^ 1);
+            load_step(n2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        write_a(SL ^ 1);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
