@@ -38,11 +38,13 @@ namespace exl3 {
 constexpr int FAT_THREADS = 256;  // 4 waves x 32 output columns
 constexpr int FAT_CH = 4;         // steps per staged A chunk (256 k)
 constexpr int FAT_ROWB = FAT_CH * 4 * 2 * 16 + 16;  // bytes per staged A row (+16: bank spread)
-// 16-row tiles stage 8 steps per chunk (16.6 KB of LDS, half the barriers;
-// their ~75 VGPRs bound the occupancy first): config 3 gate/up M = 16 29.3 ->
-// 28.6 us, exl3_gemm n = 28672 M = 16 30.2 -> 29.4.  A partial last chunk is
-// fine: its missing slices stage zeros and its steps are skipped.
-template <int MT> __host__ __device__ constexpr int fat_ch() { return MT == 16 ? 8 : FAT_CH; }
+// 16-row tiles stage 16 steps per chunk (33 KB of LDS: a 16-step k-split
+// stages its whole A range once, with no barrier and reload in the middle of
+// its steps; LDS then holds a CU to 4 workgroups): config 3 gate/up M = 16,
+// kernel alone, graph-timed, 4 / 8 / 16 steps per chunk: 29.3 / 28.6 us (op)
+// and 26.7 -> 26.1 us (kernel, 8 -> 16).  A partial last chunk is fine: its
+// missing slices stage zeros and its steps are skipped.
+template <int MT> __host__ __device__ constexpr int fat_ch() { return MT == 16 ? 16 : FAT_CH; }
 template <int MT> __host__ __device__ constexpr int fat_rowb() { return fat_ch<MT>() * 4 * 2 * 16 + 16; }
 
 // A run of rows of one expert in compact (expert-sorted) order: one row tile
@@ -298,7 +300,11 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
         const int S = gridDim.z, proj = p.gu ? (int)(blockIdx.x & 1) : 0;
         const size_t rs = (size_t)p.M * 128;  // between splits
         float* part = p.partials + ((size_t)(bx * np + proj) * S + sidx) * rs + (size_t)m0 * 128;
-        for (int idx = tid; idx < rows * 128; idx += FAT_THREADS) coherent_store(part + idx, ct[idx]);
+        for (int idx = 2 * tid; idx < rows * 128; idx += 2 * FAT_THREADS) {
+            const float2 v2 = make_float2(ct[idx], ct[idx + 1]);
+            __hip_atomic_store(reinterpret_cast<unsigned long long*>(part + idx), *reinterpret_cast<const unsigned long long*>(&v2),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         wait_stores();
         __syncthreads();
         __shared__ int gu_last;
@@ -313,6 +319,50 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
         if (!p.gu) {
             const float* pv = p.partials + (size_t)bx * S * rs + (size_t)m0 * 128 + 2 * lane;
             const float sva = __low2float(svv), svb = __high2float(svv);
+            if (S <= 4) {
+                // the gate/up epilogue's pipelining below, one projection
+                const int nchk = p.k >> 7;
+                struct RowLoads1 {
+                    float2 v[4];
+                    float rs;
+                };
+                auto issue = [&](int row, RowLoads1& L) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        L.v[t] = t < S ? coherent_load2(pv + row * 128 + (size_t)t * rs) : make_float2(0.f, 0.f);
+                    L.rs = 0.f;
+                    if constexpr (RAW) {
+                        const float* r = p.rowsum + (size_t)(m0 + row) * nchk;
+                        for (int c = lane; c < nchk; c += 64) L.rs += gptr(r)[c];
+                    }
+                };
+                auto consume = [&](int row, const RowLoads1& L) {
+                    float va = 0.f, vb = 0.f;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        va += L.v[t].x;
+                        vb += L.v[t].y;
+                    }
+                    if constexpr (RAW) {
+                        const float sx = kMul1Bias * wave_sum(L.rs);
+                        va = va * kMul1Kinv + sx;
+                        vb = vb * kMul1Kinv + sx;
+                    }
+                    fwht128_pair_fast(va, vb, lane);
+                    st_h2(gptr(p.out16) + (size_t)(m0 + row) * p.n + c0, h2_rn((va * kHadNorm) * sva, (vb * kHadNorm) * svb));
+                };
+                constexpr int RS = FAT_THREADS / 64;
+                RowLoads1 la, lb;
+                if (cw < rows) issue(cw, la);
+                for (int row = cw; row < rows; row += 2 * RS) {
+                    if (row + RS < rows) issue(row + RS, lb);
+                    consume(row, la);
+                    if (row + RS >= rows) break;
+                    if (row + 2 * RS < rows) issue(row + 2 * RS, la);
+                    consume(row + RS, lb);
+                }
+                return;
+            }
             for (int row = cw; row < rows; row += FAT_THREADS / 64) {
                 const float* const src[1] = {pv + row * 128};
                 float2 v2[1];
@@ -332,17 +382,9 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
         const float* pu = p.partials + (size_t)(bx * 2 + 1) * S * rs + (size_t)m0 * 128 + 2 * lane;
         const __half2 svg = ld_h2(gptr(p.svh) + c0), svu = ld_h2(gptr(p.svh2) + c0);
         const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
-        for (int row = cw; row < rows; row += FAT_THREADS / 64) {
-            // both columns of both projections in groups of 4 splits (16
-            // values and 8 addresses in flight: with 8 splits per group this
-            // loop set the kernel's register budget)
-            const float* const src[2] = {pg + row * 128, pu + row * 128};
-            float2 gu2[2];
-            sum_splits2<2, 4>(src, rs, S, gu2);
-            float ga = gu2[0].x, gb = gu2[0].y, ua = gu2[1].x, ub = gu2[1].y;
+        // sums -> (mul1 map) -> both output rotations, svh, SwiGLU, fp16 row
+        auto finish = [&](int row, float ga, float gb, float ua, float ub, float sx) {
             if constexpr (RAW) {
-                // both projections read the same rows: one sum over all of k
-                const float sx = kMul1Bias * fat_row_sum(p.rowsum, p.k >> 7, m0 + row, 0, p.k >> 7, lane);
                 ga = ga * kMul1Kinv + sx;
                 gb = gb * kMul1Kinv + sx;
                 ua = ua * kMul1Kinv + sx;
@@ -361,6 +403,66 @@ __global__ __launch_bounds__(FAT_THREADS, MT <= 64 ? 4 : 1) void fat_gemm_kernel
                 ub = fminf(fmaxf(ub, -p.limit), p.limit);
             }
             st_h2(gptr(p.out16) + (size_t)(m0 + row) * p.n + c0, h2_rn(silu_f(ga) * ua, silu_f(gb) * ub));
+        };
+        constexpr int RS = FAT_THREADS / 64;  // rows apart of one wave's rows
+        if (S <= 4) {
+            // up to 4 splits: a row's loads (both projections, every split,
+            // its row sums) are requested before the wave's previous row is
+            // finished, so the rows' round trips overlap (config 3 M = 16,
+            // kernel alone: 26.7 -> 26.0 us).  Two named buffers keep the
+            // loads in registers.
+            const int nchk = p.k >> 7;
+            struct RowLoads {
+                float2 v[2][4];
+                float rs;
+            };
+            auto issue = [&](int row, RowLoads& L) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        L.v[j][t] = t < S ? coherent_load2((j ? pu : pg) + row * 128 + (size_t)t * rs) : make_float2(0.f, 0.f);
+                L.rs = 0.f;
+                if constexpr (RAW) {
+                    const float* r = p.rowsum + (size_t)(m0 + row) * nchk;
+                    for (int c = lane; c < nchk; c += 64) L.rs += gptr(r)[c];
+                }
+            };
+            auto consume = [&](int row, const RowLoads& L) {
+                // split order, as sum_splits2
+                float2 gs = make_float2(0.f, 0.f), us = make_float2(0.f, 0.f);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    gs.x += L.v[0][t].x;
+                    gs.y += L.v[0][t].y;
+                    us.x += L.v[1][t].x;
+                    us.y += L.v[1][t].y;
+                }
+                float sx = 0.f;
+                if constexpr (RAW) sx = kMul1Bias * wave_sum(L.rs);
+                finish(row, gs.x, gs.y, us.x, us.y, sx);
+            };
+            RowLoads la, lb;
+            if (cw < rows) issue(cw, la);
+            for (int row = cw; row < rows; row += 2 * RS) {
+                if (row + RS < rows) issue(row + RS, lb);
+                consume(row, la);
+                if (row + RS >= rows) break;
+                if (row + 2 * RS < rows) issue(row + 2 * RS, la);
+                consume(row + RS, lb);
+            }
+            return;
+        }
+        for (int row = cw; row < rows; row += RS) {
+            // both columns of both projections in groups of 4 splits (16
+            // values and 8 addresses in flight: with 8 splits per group this
+            // loop set the kernel's register budget)
+            const float* const src[2] = {pg + row * 128, pu + row * 128};
+            float2 gu2[2];
+            sum_splits2<2, 4>(src, rs, S, gu2);
+            float sx = 0.f;
+            if constexpr (RAW) sx = kMul1Bias * fat_row_sum(p.rowsum, p.k >> 7, m0 + row, 0, p.k >> 7, lane);
+            finish(row, gu2[0].x, gu2[0].y, gu2[1].x, gu2[1].y, sx);
         }
         return;
     }
