@@ -381,8 +381,45 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
             }
         }
     };
+    // Rows that arrive rotated (read plainly, not by the fused launch's
+    // coherent loads): each lane loads its V = NS * KW consecutive k values of
+    // a row (kts_wg * 16 / 64) with one set of loads, all of the wave's rows
+    // at once, so staging costs one round trip (the block-at-a-time loop
+    // below waits a round trip per (row, 128-block) after the first two:
+    // up to ~9 us for a 16-row unit at B = 16).  Chunks of 128 % V != 0 with
+    // mul1 chunk sums stay on that loop.
+    constexpr int V = NS * KW;
+    constexpr int RPW = (MOE_UNIT_ROWS + 4 * KW - 1) / (4 * KW);  // rows per wave at most
+    constexpr bool vec_stage = pre_rotated && !wait_h && V % 2 == 0 && V <= 16 && (CB != 2 || 128 % V == 0);
+    uint32_t xw[vec_stage ? RPW : 1][vec_stage ? V / 2 : 1];
+    auto vec_load = [&]() {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = wave + r * nwaves;
+            if (row < m) {
+                const EXL3_GLOBAL uint32_t* src =
+                    reinterpret_cast<const EXL3_GLOBAL uint32_t*>(x_row(row) + kt_wg0 * 16 + lane * V);
+                if constexpr (V % 8 == 0) {
+#pragma unroll
+                    for (int c = 0; c < V / 8; ++c) {
+                        const u32x4_t q = reinterpret_cast<const EXL3_GLOBAL u32x4_t*>(src)[c];
+                        xw[r][4 * c] = q.x;
+                        xw[r][4 * c + 1] = q.y;
+                        xw[r][4 * c + 2] = q.z;
+                        xw[r][4 * c + 3] = q.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < V / 2; ++c) xw[r][c] = src[c];
+                }
+            }
+        }
+    };
     uint32_t w[gv_depth<K>()][K];
-    if constexpr (wait_h) {
+    if constexpr (vec_stage) {
+        vec_load();
+        prime_weights<K, NS>(w, tiles(bx0), step_stride);
+    } else if constexpr (wait_h) {
         if (!p.prime_late) prime_weights<K, NS>(w, tiles(bx0), step_stride);
         if (tid == 0 && !wait_ready(p.ready + (size_t)u * p.ready_stride, kt_wg0 >> 3, (kt_wg0 + kts_wg - 1) >> 3,
                                     p.ready_target, p.poll_sleep, p.max_polls))
@@ -423,6 +460,31 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
             if (lane == 0) xsum[b] = t;
         }
     };
+    if constexpr (vec_stage) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = wave + r * nwaves;
+            if (row < m) {
+                float sx = 0.f;
+#pragma unroll
+                for (int c = 0; c < V / 2; ++c) {
+                    const uint32_t bits = xw[r][c];
+                    const uint32_t da = __builtin_amdgcn_perm(bits, bits, 0x01000100u);  // (a, a)
+                    const uint32_t dc = __builtin_amdgcn_perm(bits, bits, 0x03020302u);  // (c, c)
+                    *reinterpret_cast<uint2*>(xs + xs_index(lane * V + 2 * c, row, kts_wg)) = make_uint2(da, dc);
+                    if constexpr (CB == 2)
+                        sx += __half2float(__ushort_as_half((unsigned short)(bits & 0xffffu))) +
+                              __half2float(__ushort_as_half((unsigned short)(bits >> 16)));
+                }
+                if constexpr (CB == 2) {
+                    // chunk sum over the 128 / V lanes of each 128-wide block
+#pragma unroll
+                    for (int o = 1; o < 128 / V; o <<= 1) sx += __shfl_xor(sx, o);
+                    if ((lane & (128 / V - 1)) == 0) xsum[row * nblk128 + lane * V / 128] = sx;
+                }
+            }
+        }
+    } else {
 #pragma unroll
     for (int j = 0; j < MV_PRE; ++j) {
         const int b = wave + j * nwaves;
@@ -434,6 +496,7 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
         const __half2 sv = pre_rotated ? __half2{} : ld_h2_ptr(suh, kg);
         const __half2 uv = (down && GFX) ? ld_x(x_row(row) + up_rows + kg) : __half2{};
         stage(b, ld_x(x_row(row) + kg), uv, sv);
+    }
     }
     __syncthreads();
     if constexpr (wait_h && FXS) {
