@@ -118,8 +118,16 @@ __device__ __forceinline__ __half2 h2_rn(float a, float b) {
 }
 
 // SiLU in fp32, g * sigmoid(g) = g / (1 + e^-g) (the reference's SwiGLU:
-// csrc/p2b_moe.cu:283-290, src/sglang_exl3/exl3.py:1199-1206).
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+// csrc/p2b_moe.cu:283-290, src/sglang_exl3/exl3.py:1199-1206), with e^-g as
+// 2^(-g log2 e) and the quotient as g times a reciprocal, from the hardware's
+// exp2 and reciprocal approximations (v_exp_f32, v_rcp_f32, about 1 ulp
+// each): a few ulp of fp32 error, far below the fp16 rounding every caller
+// applies, and 4 VALU ops instead of ~20 for a correctly rounded exp and
+// divide (the wide-tile gate/up epilogue runs 64 of these per lane per tile).
+// e^-g overflowing to inf gives 0 (g -> -inf), e^-g -> 0 gives g.
+__device__ __forceinline__ float silu_f(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
 
 // +1.0f where bit J of lane is clear, -1.0f where it is set.
 template <int J>
