@@ -193,16 +193,21 @@ __device__ __forceinline__ void fwht128_pair_fast(float& a, float& b, int lane) 
 
 // The same transform with one row held as 16 consecutive values per lane over
 // 8 lanes (value 16 (lane & 7) + e in v[e]): stages of stride 1 .. 8 in
-// registers, 16 .. 64 across the lanes (xor 1, 2, 4), in the same order and
-// with the same float operations as fwht128_pair_f (x + y below, x - y above;
-// fma(v, -1, p) is p - v exactly).
-template <int J>
-__device__ __forceinline__ void fwht_x16_stage(float (&v)[16], int lane) {
-    const float sg = (lane & J) ? -1.f : 1.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) v[e] = __builtin_fmaf(v[e], sg, lane_xor<J>(v[e]));
-}
-
+// registers, 16 .. 64 across the lanes (xor 1, 2, 4), in the order of
+// fwht128_pair_f and with the same rounded magnitudes; like fwht128_pair_fast,
+// a result that is exactly zero may differ in sign.  The lane stages run on
+// values that carry a sign, as in fwht128_pair_fast: lane L forms v + c p with
+// the partner's value p as the DPP operand of one v_fmac (c = -1 where bit J
+// of L is set), which is x + y on the lower lane and -(x - y) on the upper one.
+// Both lanes of every later pair carry the same sign, so after the three
+// stages lane L holds (-1)^popcount(L & 7) times the transform, and
+// fwht_x16_norm(L) is that sign times 1/sqrt(128).  One asm block per stage:
+// the compiler does not fold a DPP move into v_fmac, and a VGPR written by a
+// VALU op needs two wait states before a DPP read of it (the leading s_nop;
+// inside a block each register is read 16 instructions after it is written).
+#define EXL3_R16(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15)
+#define EXL3_X16_V(i) [v##i] "+v"(v[i]),
+#define EXL3_X16_T(i) [t##i] "=&v"(t[i]),
 __device__ __forceinline__ void fwht128_x16(float (&v)[16], int lane) {
 #pragma unroll
     for (int h = 1; h < 16; h <<= 1)
@@ -213,9 +218,35 @@ __device__ __forceinline__ void fwht128_x16(float (&v)[16], int lane) {
                 v[e] = x + y;
                 v[e | h] = x - y;
             }
-    fwht_x16_stage<1>(v, lane);
-    fwht_x16_stage<2>(v, lane);
-    fwht_x16_stage<4>(v, lane);
+    // the signs are listed as in-out operands only to close the operand lists
+    float c1 = lane_sign<1>(lane), c2 = lane_sign<2>(lane), c4 = lane_sign<4>(lane);
+    asm("s_nop 1\n\t"
+#define EXL3_X16_S(i) "v_fmac_f32_dpp %[v" #i "], %[v" #i "], %[c] quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        EXL3_R16(EXL3_X16_S)
+#undef EXL3_X16_S
+        : EXL3_R16(EXL3_X16_V) [c] "+v"(c1));
+    asm("s_nop 1\n\t"
+#define EXL3_X16_S(i) "v_fmac_f32_dpp %[v" #i "], %[v" #i "], %[c] quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        EXL3_R16(EXL3_X16_S)
+#undef EXL3_X16_S
+        : EXL3_R16(EXL3_X16_V) [c] "+v"(c2));
+    // lane ^ 4 = (lane ^ 7) ^ 3: row_half_mirror, then quad_perm [3,2,1,0]
+    float t[16];
+    asm("s_nop 1\n\t"
+#define EXL3_X16_M(i) "v_mov_b32_dpp %[t" #i "], %[v" #i "] row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        EXL3_R16(EXL3_X16_M)
+#undef EXL3_X16_M
+#define EXL3_X16_S(i) "v_fmac_f32_dpp %[v" #i "], %[t" #i "], %[c] quad_perm:[3,2,1,0] row_mask:0xf bank_mask:0xf\n\t"
+        EXL3_R16(EXL3_X16_S)
+#undef EXL3_X16_S
+        : EXL3_R16(EXL3_X16_V) EXL3_R16(EXL3_X16_T) [c] "+v"(c4));
+}
+#undef EXL3_X16_T
+#undef EXL3_X16_V
+#undef EXL3_R16
+
+__device__ __forceinline__ float fwht_x16_norm(int lane) {
+    return (__builtin_popcount(lane & 7) & 1) ? -kHadNorm : kHadNorm;
 }
 
 // Sum of v over the 64 lanes of the wave (every lane gets the same total,

@@ -873,6 +873,7 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
             }
             fwht128_x16(gv, lane);
             fwht128_x16(uv, lane);
+            const float hn = fwht_x16_norm(lane);
             const int c0 = bx * 128 + col;
             const EXL3_GLOBAL uint32_t* sgp = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh) + c0);
             const EXL3_GLOBAL uint32_t* sup = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh2) + c0);
@@ -885,8 +886,8 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int e = 2 * e2 + h;
-                    float gg = (gv[e] * kHadNorm) * __half2float(__ushort_as_half((unsigned short)(sgw >> (16 * h))));
-                    float uu = (uv[e] * kHadNorm) * __half2float(__ushort_as_half((unsigned short)(suw >> (16 * h))));
+                    float gg = (gv[e] * hn) * __half2float(__ushort_as_half((unsigned short)(sgw >> (16 * h))));
+                    float uu = (uv[e] * hn) * __half2float(__ushort_as_half((unsigned short)(suw >> (16 * h))));
                     if (clamp) {
                         gg = fminf(gg, p.limit);
                         uu = fminf(fmaxf(uu, -p.limit), p.limit);
@@ -921,6 +922,7 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
                 v[4 * q + 3] = t.w;
             }
             fwht128_x16(v, lane);
+            const float hn = fwht_x16_norm(lane);
             const int c0 = bx * FB_COLS + col;
             // svh and the outputs are only 4- (8-) byte aligned by contract
             const EXL3_GLOBAL uint32_t* svp = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh) + c0);
@@ -930,7 +932,7 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const __half sv = __ushort_as_half((unsigned short)(sw[e >> 1] >> (16 * (e & 1))));
-                v[e] = (v[e] * kHadNorm) * __half2float(sv);
+                v[e] = (v[e] * hn) * __half2float(sv);
             }
             if (p.accumulate) {
                 // atomics want a wave's lanes on consecutive columns: the
