@@ -39,6 +39,11 @@ extern "C" {
 #define EXL3_WAIT_MOE_FUSED 1 /* one-launch one-token MoE: a down item's wait for its h blocks */
 #define EXL3_WAIT_FAT_TAIL 2  /* wide-tile GEMM tail split: the second k-half's wait for the first */
 
+/* Element types of exl3_hadamard_fast. */
+#define EXL3_DTYPE_F16 0
+#define EXL3_DTYPE_BF16 1
+#define EXL3_DTYPE_F32 2
+
 #define EXL3_CB_3INST 0
 #define EXL3_CB_MCG 1
 #define EXL3_CB_MUL1 2
@@ -78,10 +83,20 @@ int exl3_decode_tiles(const int16_t* trellis, uint16_t* W, int k, int n, int K, 
  * with H the unnormalised Sylvester matrix (scale = 1/sqrt(128) normalises);
  * pre / post may be NULL (no scaling).  x, y: f16 [rows][cols], cols a
  * multiple of 128; y may alias x.  Replaces exllamav3's had_r_128 as called by
- * src/sglang_exl3/exl3.py:1184-1228 and the matmul of transform_hadamard_fast
- * (src/sglang_exl3/hadamard_cache.py:89-120). */
+ * src/sglang_exl3/exl3.py:1184-1228. */
 int exl3_hadamard_rows(const uint16_t* x, uint16_t* y, const uint16_t* pre, const uint16_t* post, float scale,
                        int rows, int cols, void* stream);
+
+/* transform_hadamard_fast in the caller's element type T (EXL3_DTYPE_F16,
+ * _BF16 or _F32): per 128-column block,
+ *   y[r][128c + j] = T( T( sum_i x[r][128c + i] H[i][j] h ) * post[128c + j] )
+ * with H the Sylvester matrix, h = 1/sqrt(128) rounded to fp32 and then to T,
+ * the sum in fp32 (here in FWHT order), and post (suh converted to T) may be
+ * NULL (then y is the first rounding).  x, y, post: T [rows][cols] / [cols],
+ * cols a multiple of 128, y may alias x.  Replaces the fp16 (bf16, fp32)
+ * torch.matmul by the cached Hadamard matrix and the suh product of
+ * transform_hadamard_fast (src/sglang_exl3/hadamard_cache.py:88-120). */
+int exl3_hadamard_fast(const void* x, void* y, const void* post, int rows, int cols, int dtype, void* stream);
 
 /* Scratch bytes exl3_gemv / exl3_gemm / exl3_p2b_gemv_batched need for a
  * problem of `experts` independent GEMVs of [m,k]x[k,n].  The workspace must

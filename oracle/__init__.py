@@ -197,6 +197,51 @@ def had_rows(x: np.ndarray, pre: Optional[np.ndarray], post: Optional[np.ndarray
     return y
 
 
+def round_bf16(a: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 (ties to even), returned as float32 (finite inputs)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def round_to(a: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 values rounded to dtype ("f16", "bf16", "f32"), returned as float32."""
+    a = np.asarray(a, dtype=np.float32)
+    if dtype == "f16":
+        return a.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        return round_bf16(a)
+    return a
+
+
+def sylvester(n: int = 128) -> np.ndarray:
+    """Unnormalised Sylvester-Hadamard matrix built by the reference's doubling
+    [[H, H], [H, -H]] (src/sglang_exl3/hadamard_cache.py:105-108)."""
+    H = np.ones((1, 1))
+    while H.shape[0] < n:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+def had_fast(x: np.ndarray, post: Optional[np.ndarray], dtype: str) -> np.ndarray:
+    """transform_hadamard_fast (src/sglang_exl3/hadamard_cache.py:88-120) in
+    dtype ("f16", "bf16", "f32"): each 128-block times the Sylvester matrix of
+    +-h, h = 1/sqrt(128) rounded to fp32 and then to dtype (:109), the block
+    sum taken exactly (float64: the products x h are exact, and so is the sum
+    of 128 of them for operands of a few binades) and rounded to fp32, then to
+    dtype (the matmul's output); then times post (suh converted to dtype, :116)
+    and rounded to dtype again.  x holds dtype values as float32."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = a.shape
+    h = float(round_to(np.float32([1.0 / 128.0 ** 0.5]), dtype)[0])
+    blocks = a.astype(np.float64).reshape(rows, cols // 128, 128)
+    s = np.einsum("rbi,ij->rbj", blocks, sylvester() * h).reshape(rows, cols)
+    y = round_to(s.astype(np.float32), dtype)
+    if post is not None:
+        y = round_to(y * round_to(np.asarray(post, dtype=np.float32), dtype), dtype)
+    return y
+
+
 def f16_to_f32(bits: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(bits).view(np.float16).astype(np.float32)
 

@@ -23,6 +23,11 @@ EXL3_ERR_WORKSPACE = 4
 EXL3_WAIT_MOE_FUSED = 1
 EXL3_WAIT_FAT_TAIL = 2
 
+# element types of exl3_hadamard_fast
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+DTYPE_F32 = 2
+
 CB_3INST = 0
 CB_MCG = 1
 CB_MUL1 = 2
@@ -46,6 +51,7 @@ SIGNATURES = {
     "exl3_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_p2b_gemv_batched": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "exl3_hadamard_rows": (_I, [_P, _P, _P, _P, _F, _I, _I, _P]),
+    "exl3_hadamard_fast": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "exl3_gemm_workspace_size": (_SZ, [_I, _I, _I, _I]),
     "exl3_fat_gemm": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "exl3_fat_gemm_scatter": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

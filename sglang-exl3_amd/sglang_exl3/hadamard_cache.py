@@ -6,8 +6,10 @@ Same surface as the reference module (src/sglang_exl3/hadamard_cache.py:1-120):
 hit/miss counters, gated by SGLANG_OPT_MOE_QUANT_ONCE), the process-wide
 instance, and ``transform_hadamard_fast`` (rows in blocks of 128, normalised
 Hadamard, optional post-scale by suh).  The transform runs the gfx950 kernel
-behind ``exl3_hadamard_rows`` in one fp32 pass (the reference does an fp16
-matmul by H/sqrt(128), then the suh product: at most a rounding apart).
+behind ``exl3_hadamard_fast`` in x's dtype (fp16, bf16, fp32) with the
+reference's scale and roundings; only the order of the fp32 block sum differs
+from the reference's matmul.  ``hadamard_rows`` is the fp16 row transform with
+pre/post scales that the expert paths use (exllamav3's had_r_128).
 """
 
 from __future__ import annotations
@@ -123,17 +125,33 @@ def hadamard_rows(x: torch.Tensor, pre: Optional[torch.Tensor] = None, post: Opt
     return y
 
 
+_FAST_DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+
+
 def transform_hadamard_fast(x: torch.Tensor, suh: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Row-wise normalised Walsh-Hadamard transform in blocks of 128, then the
-    optional suh post-scale (src/sglang_exl3/hadamard_cache.py:89-120).  Widths
+    optional suh product, in x's dtype (src/sglang_exl3/hadamard_cache.py:88-120):
+    the block sums are scaled by 1/sqrt(128) rounded to that dtype and rounded
+    to it, then multiplied by suh converted to it and rounded again, as the
+    reference's matmul by its cached matrix and its suh product do.  Widths
     that are not multiples of 128 come back unchanged, as in the reference.
-    Other dtypes are converted to fp16 for the kernel and back."""
+    fp16, bf16 and fp32 HIP tensors."""
     hidden = int(x.shape[-1])
     if hidden % 128:
         return x
+    code = _FAST_DTYPES.get(x.dtype)
+    if code is None:
+        raise RuntimeError(f"sglang_exl3 transform_hadamard_fast: dtype {x.dtype} (fp16, bf16 or fp32)")
+    if not x.is_cuda:
+        raise RuntimeError("sglang_exl3 transform_hadamard_fast requires HIP device tensors")
     post = None
     if suh is not None and suh.numel() == hidden:
-        post = suh.reshape(-1).to(device=x.device, dtype=torch.float16)
-    xh = x.reshape(-1, hidden).to(torch.float16)
-    y = hadamard_rows(xh, None, post, HAD_NORM)
-    return y.to(x.dtype).view_as(x)
+        post = suh.reshape(-1).to(device=x.device, dtype=x.dtype).contiguous()
+    xc = x.reshape(-1, hidden).contiguous()
+    y = torch.empty_like(xc)
+    with torch.cuda.device(x.device):
+        rc = _lib.lib().exl3_hadamard_fast(xc.data_ptr(), y.data_ptr(), None if post is None else post.data_ptr(),
+                                           int(xc.shape[0]), hidden, code,
+                                           int(torch.cuda.current_stream(x.device).cuda_stream))
+    _lib.check(rc, "exl3_hadamard_fast")
+    return y.view_as(x)

@@ -57,6 +57,17 @@ def test_dequant_rejects_bad_arguments():
     assert b"k=100" in L.exl3_last_error()
 
 
+def test_hadamard_fast_rejects_bad_arguments():
+    L = _lib.lib()
+    assert L.exl3_hadamard_fast(None, None, None, 1, 128, 3, None) == _lib.EXL3_ERR_ARG
+    assert b"dtype=3" in L.exl3_last_error()
+    assert L.exl3_hadamard_fast(None, None, None, 1, 100, _lib.DTYPE_BF16, None) == _lib.EXL3_ERR_ARG
+    assert b"cols=100" in L.exl3_last_error()
+    assert L.exl3_hadamard_fast(None, None, None, 2, 128, _lib.DTYPE_F32, None) == _lib.EXL3_ERR_ARG
+    assert b"null pointer" in L.exl3_last_error()
+    assert L.exl3_hadamard_fast(None, None, None, 0, 128, _lib.DTYPE_F16, None) == _lib.EXL3_OK
+
+
 def test_batched_rejects_bad_arguments():
     L = _lib.lib()
     rc = L.exl3_p2b_gemv_batched(None, 0, None, None, None, None, 0, None, 1, 2048, 768, 3, 1, None, 0, None)

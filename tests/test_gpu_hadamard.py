@@ -1,6 +1,8 @@
-"""GPU parity of the row Hadamard transform (exl3_hadamard_rows) against the
-oracle: bit-exact fp16 (same fp32 operations in the same order, one final
-rounding), including the DPP / permlane lane exchanges of every FWHT stage."""
+"""GPU parity of the row Hadamard transforms against the oracle:
+exl3_hadamard_rows bit-exact in fp16 (same fp32 operations in the same order,
+one final rounding), including the DPP / permlane lane exchanges of every FWHT
+stage; exl3_hadamard_fast (transform_hadamard_fast) in fp16, bf16 and fp32
+with the reference's scale and roundings."""
 
 import numpy as np
 import pytest
@@ -39,6 +41,57 @@ def test_hadamard_rows_in_place_and_lane_layout():
     while H.shape[0] < 128:
         H = np.block([[H, H], [H, -H]])
     assert np.array_equal(x.float().cpu().numpy(), H)
+
+
+_TDT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("rows,cols,post_kind", [(1, 128, None), (5, 512, "sign"), (33, 4096, "mixed"),
+                                                 (1000, 256, "sign"), (2, 384, "mixed")])
+def test_transform_hadamard_fast_matches_oracle(dtype, rows, cols, post_kind):
+    """exl3_hadamard_fast against oracle.had_fast (exact block sum, the
+    reference's dtype-rounded scale and its two roundings).  Only the fp32
+    block sum's order differs (FWHT stages here, a matmul in the reference),
+    so fp16 / bf16 results are bit-identical except where the exact value lies
+    within a few fp32 ulps of a rounding boundary (then one ulp apart, for at
+    most 2e-3 of the elements), and fp32 results lie within the FWHT's
+    rounding bound, 8 ulps of sum |x| h."""
+    print(f"case: hadamard_fast dtype={dtype} rows={rows} cols={cols} post={post_kind}", flush=True)
+    rng = np.random.default_rng(rows * 13 + cols + len(dtype))
+    x = oracle.round_to(rng.standard_normal((rows, cols)).astype(np.float32) * 3.0, dtype)
+    post = None
+    if post_kind == "sign":
+        post = rng.choice([-1.0, 1.0], cols).astype(np.float32)
+    elif post_kind == "mixed":
+        post = rng.choice([-1.0, 1.0, 0.5, -2.0, 1.5, 0.7], cols).astype(np.float32)
+    xt = torch.from_numpy(x).to(_TDT[dtype]).cuda()
+    suh = None if post is None else torch.from_numpy(post).half().cuda()
+    y = transform_hadamard_fast(xt, suh)
+    torch.cuda.synchronize()
+    assert y.dtype == xt.dtype and y.shape == xt.shape
+    got = y.float().cpu().numpy()
+    want = oracle.had_fast(x, None if post is None else post.astype(np.float16), dtype)
+    if dtype == "f32":
+        h = float(np.float32(0.08838834764831845))
+        mag = np.repeat(np.abs(x).reshape(rows, cols // 128, 128).sum(-1), 128, axis=1) * h
+        if post is not None:
+            mag = mag * np.abs(post)[None, :]
+        assert np.all(np.abs(got - want) <= 8 * 2.0 ** -24 * mag + 1e-30)
+        return
+    diff = got != want
+    assert diff.mean() <= 2e-3, f"{int(diff.sum())} of {diff.size} differ"
+    mbits = 10 if dtype == "f16" else 7
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-30))) - mbits)
+    assert np.all(np.abs(got - want)[diff] <= ulp[diff])
+
+
+def test_transform_hadamard_fast_rejects_other_dtypes():
+    with pytest.raises(RuntimeError, match="dtype"):
+        transform_hadamard_fast(torch.zeros((1, 128), dtype=torch.float64, device="cuda"))
+    L = _lib.lib()
+    assert L.exl3_hadamard_fast(None, None, None, 1, 128, 3, None) == _lib.EXL3_ERR_ARG
+    assert L.exl3_hadamard_fast(None, None, None, 1, 100, 0, None) == _lib.EXL3_ERR_ARG
 
 
 def test_transform_hadamard_fast_involution_and_suh():

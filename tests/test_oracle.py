@@ -153,6 +153,67 @@ def test_fwht_matches_reference_header_bitwise():
         assert np.array_equal(oracle.fwht(v).view(np.uint32), b.view(np.uint32))
 
 
+# ------------------------------------------- transform_hadamard_fast (had_fast)
+
+def test_round_bf16_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(11)
+    a = (rng.standard_normal(4096) * np.exp2(rng.integers(-20, 20, 4096))).astype(np.float32)
+    # exact ties: bit 15 set, bits 0..14 clear, both parities of bit 16
+    ties = (a.view(np.uint32) & np.uint32(0xFFFF0000)) | np.uint32(0x8000)
+    a = np.concatenate([a, ties.view(np.float32), np.float32([0.0, -0.0, 1.0, -3.5])])
+    want = torch.from_numpy(a).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(oracle.round_bf16(a).view(np.uint32), want.view(np.uint32))
+
+
+def test_sylvester_matches_fwht():
+    H = oracle.sylvester(128)
+    assert np.array_equal(H, _sylvester(128))
+    e = np.eye(128, dtype=np.float32)
+    assert np.array_equal(np.stack([oracle.fwht(r) for r in e]), H.astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype,h", [("f16", 181 / 2048), ("bf16", 181 / 2048), ("f32", float(np.float32(0.08838834764831845)))])
+def test_had_fast_one_hot_and_constant_rows(dtype, h):
+    """One-hot row i gives +-h in column j with the sign of H[i][j] (exactly the
+    dtype's 1/sqrt(128)); a row of ones gives T(128 h) in column 0 of each block
+    and zeros elsewhere."""
+    H = oracle.sylvester(128)
+    x = np.eye(256, dtype=np.float32)[:256:37]
+    y = oracle.had_fast(x, None, dtype)
+    for r, i in enumerate(range(0, 256, 37)):
+        blk = i // 128
+        want = np.zeros(256)
+        want[blk * 128:(blk + 1) * 128] = H[i % 128] * h
+        assert np.array_equal(y[r], want.astype(np.float32))
+    ones = oracle.had_fast(np.ones((1, 256), np.float32), None, dtype)
+    want = np.zeros(256, np.float32)
+    want[[0, 128]] = oracle.round_to(np.float32(128 * h), dtype)
+    assert np.array_equal(ones[0], want)
+
+
+def test_had_fast_rounds_twice_around_post():
+    """x = 3 e_0, post[0] = p: y[0] = T(T(3h) p), not T(3h p) (two roundings,
+    the reference's matmul output and then its suh product)."""
+    h = 181 / 2048
+    p = np.float16(1.0009765625)  # 1 + 2^-10
+    x = np.zeros((1, 128), np.float32)
+    x[0, 0] = 3.0
+    post = np.ones(128, np.float16)
+    post[0] = p
+    y = oracle.had_fast(x, post, "f16")
+    t = np.float16(np.float32(3 * h))
+    assert y[0, 0] == np.float16(np.float32(t) * np.float32(p))
+    assert np.array_equal(y[0, 1:], np.float32(t) * oracle.sylvester(128)[0, 1:].astype(np.float32))
+
+
+def test_had_fast_is_near_involution_in_f32():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((3, 384)).astype(np.float32)
+    back = oracle.had_fast(oracle.had_fast(x, None, "f32"), None, "f32")
+    assert np.allclose(back, x, rtol=1e-5, atol=1e-5)
+
+
 # ------------------------------------------------------------------- dequant
 
 @pytest.mark.parametrize("tag", ["K2_mcg", "K3_mul1", "K4_mcg", "K4_mul1", "K5_mcg", "K8_mul1"])
