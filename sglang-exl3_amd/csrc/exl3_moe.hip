@@ -361,19 +361,24 @@ double expected_active(int tokens, int topk, int E) {
 //  * column blocks per item grouped only when the items would exceed
 //    8 x 512 (a few per workgroup of the persistent grid).
 // Env overrides (tuning): EXL3_MOE_NSTEPS, EXL3_MOE_KW, EXL3_MOE_BPI.
-MoePlan plan_moe(double units, int entries, int k, int n, int nproj) {
+MoePlan plan_moe(double units, int entries, int k, int n, int nproj, double items12) {
     (void)entries;
     const int kslices = k / 16, nblk = n / 128;
     const double grid = 512.0;
     int kw = env_int("EXL3_MOE_KW", 1);
     if (kw != 1 && kw != 2) kw = 1;
-    // 12-step items (48 k-slices) when k allows and the pass has work for
-    // 1.5 rounds of the ~1024-workgroup grid even so: fewer splits, so fewer
-    // hand-offs and partial sums (down pass, config 4 B = 64: 98.9 -> 92.6 us,
-    // config 5 K = 2: 109.1 -> 103.9 us; with less work the fewer, longer items
-    // leave workgroups idle: config 4 B = 16: 49.9 -> 54.2 us)
+    // 12-step items (48 k-slices) when k allows and the pass has at least
+    // `items12` of them: fewer splits, so fewer hand-offs and partial sums,
+    // against fewer items in flight.  With partial-row hand-offs that pays
+    // from 1.5 rounds of the ~1024-workgroup grid (down pass, config 4 B = 64:
+    // 98.9 -> 92.6 us, config 5 K = 2: 109.1 -> 103.9 us); in the down pass
+    // with the fused fixed-point combine every split costs its adds, and it
+    // pays from ~700 items (config 4, graph-timed, 4 -> 12 steps: B = 7 / 8 /
+    // 12 / 16 with 744 / 816 / 1097 / 1318 items: 34.7 / 37.4 / 41.9 / 45.2 ->
+    // 33.4 / 35.2 / 38.4 / 42.2 us; B = 2 / 4 / 6 with 224 / 466 / 657 items:
+    // 22.3 / 27.1 / 29.4 -> 24.2 / 28.9 / 30.7 us).
     int ns = env_int(nproj == 1 ? "EXL3_MOE_DN_NSTEPS" : "EXL3_MOE_GU_NSTEPS", 0);
-    if (ns == 0 && kw == 1 && kslices % 48 == 0 && units * nblk * (kslices / 48) >= 1536.0) ns = 12;
+    if (ns == 0 && kw == 1 && kslices % 48 == 0 && units * nblk * (kslices / 48) >= items12) ns = 12;
     if (ns == 12 && kslices % (4 * ns * kw) == 0 && moe_smem_bytes(4 * ns * kw, kw) <= kMaxLds / 2 - 1024)
         return MoePlan{ns, kw, kslices / (4 * ns * kw), 1};
     if (ns <= 0 || ns == 12) ns = env_int("EXL3_MOE_NSTEPS", 8);
@@ -425,17 +430,6 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     const double act = expected_active(tokens, topk, E);
     const double per = act > 0 ? L.entries / act : 1.0;  // rows per active expert
     const double units = act * ceil(per / MOE_UNIT_ROWS);
-    L.gu = plan_moe(units, L.entries, hidden, inter, 2);
-    L.dn = plan_moe(units, L.entries, inter, hidden, 1);
-    size_t o = kWsScratchOffset;
-    L.route_off = o;
-    o = align256(o + 4 * sizeof(int));
-    L.units_off = o;
-    o = align256(o + (size_t)L.max_units * sizeof(MoeUnit));
-    L.rows_off = o;
-    o = align256(o + (size_t)L.entries * sizeof(int));
-    L.tokv_off = o;
-    o = align256(o + (size_t)tokens * sizeof(int));
     // Up to kMoeFusedCombineTokens tokens the weighted combine runs inside the
     // down pass (fixed-point output accumulators, 8 bytes per output, in the
     // workspace's accumulator region).  Graph-timed on config 4 it saves the
@@ -446,6 +440,17 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     // Env EXL3_MOE_FC_TOKENS overrides the threshold (0: never fused).
     const int fc_tokens = env_int("EXL3_MOE_FC_TOKENS", kMoeFusedCombineTokens);
     L.fc = tokens <= fc_tokens && (size_t)tokens * hidden * 8 <= kWsAccBytes && topk <= SK_MAX_CONTRIB;
+    L.gu = plan_moe(units, L.entries, hidden, inter, 2, 1536.0);
+    L.dn = plan_moe(units, L.entries, inter, hidden, 1, L.fc ? 700.0 : 1536.0);
+    size_t o = kWsScratchOffset;
+    L.route_off = o;
+    o = align256(o + 4 * sizeof(int));
+    L.units_off = o;
+    o = align256(o + (size_t)L.max_units * sizeof(MoeUnit));
+    L.rows_off = o;
+    o = align256(o + (size_t)L.entries * sizeof(int));
+    L.tokv_off = o;
+    o = align256(o + (size_t)tokens * sizeof(int));
     // h: the rotated activation rows; with the fused combine, room for the
     // fp16 gate and up rows of the split fixed-point gate/up pass instead
     L.h_off = o;
