@@ -228,8 +228,8 @@ int exl3_moe_plan(int tokens, int topk, int num_experts, int hidden, int inter, 
  *   out[t] = sum_s w[t][s] * down_e( fp16( silu(min(g, L)) * clamp(u, -L, L) ) ),
  *   e = topk_ids[t][s], g = fp16(gate_e(x[t])), u = fp16(up_e(x[t])),
  * fp16 out [tokens][hidden].  The sum over slots of w * fp16(down) is taken
- * in fp32 in slot order above 16 tokens and in 64-bit fixed point (2^-30
- * resolution) up to 16 tokens; both are deterministic.  Ids outside [0, num_experts) are
+ * in fp32 in slot order above 48 tokens and in 64-bit fixed point (2^-30
+ * resolution) up to 48 tokens; both are deterministic.  Ids outside [0, num_experts) are
  * skipped (weight ignored), like map_topk_to_local's invalid slot.  The nine
  * pointer tables are int64 device arrays of num_experts device addresses.
  * swiglu_limit <= 0 or infinite: no clamp.  K per projection 1..8, one

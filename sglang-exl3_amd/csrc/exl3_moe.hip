@@ -410,7 +410,7 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj, double item
 // on (config 4 B = 2 / 4: 27.9 / 29.4 -> 27.3 / 28.5 us; config 5 K = 2, B = 4:
 // 109.0 -> 106.0 us; K = 4: 119.2 -> 115.1 us).
 constexpr int kMoeRotTokens = 2;
-constexpr int kMoeFusedCombineTokens = 16;
+constexpr int kMoeFusedCombineTokens = 48;
 constexpr int kMoeGfxTokens = 3;  // routed batches with the split fixed-point gate/up pass
 
 struct MoeLayout {
@@ -434,10 +434,13 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     // down pass (fixed-point output accumulators, 8 bytes per output, in the
     // workspace's accumulator region).  Graph-timed on config 4 it saves the
     // combine launch (B = 1 / 2 / 4 / 8 / 16: 27.8 / 32.6 / 36.1 / 49.9 / 64.5 us
-    // -> 24.6 / 29.3 / 32.8 / 47.4 / 63.6 us); from 32 tokens the contended
-    // 64-bit atomics (eight slots per output) cost more than the launch
-    // (B = 32 / 48 / 64: 100.2 / 114.3 / 117.0 -> 105.6 / 120.1 / 123.6 us).
-    // Env EXL3_MOE_FC_TOKENS overrides the threshold (0: never fused).
+    // -> 24.6 / 29.3 / 32.8 / 47.4 / 63.6 us, with 4-step down items).  With
+    // 12-step down items (one add per output and slot, no split adds) it pays
+    // up to ~48 tokens: B = 17 / 24 / 32 / 48: 51.0 / 51.0 / 59.4 / 72.0 ->
+    // 44.0 / 47.7 / 58.4 / 68.2 us; B = 64 even (81.2 / 81.1), B = 96 / 128:
+    // 102.4 / 122.0 -> 105.8 / 128.7 us (the contended adds, eight slots per
+    // output, cost more than the launch).  Env EXL3_MOE_FC_TOKENS overrides the
+    // threshold (0: never fused).
     const int fc_tokens = env_int("EXL3_MOE_FC_TOKENS", kMoeFusedCombineTokens);
     L.fc = tokens <= fc_tokens && (size_t)tokens * hidden * 8 <= kWsAccBytes && topk <= SK_MAX_CONTRIB;
     L.gu = plan_moe(units, L.entries, hidden, inter, 2, 1536.0);

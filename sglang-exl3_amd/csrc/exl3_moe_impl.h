@@ -1,7 +1,7 @@
 // Batched routed-expert MoE layer for gfx950: every active expert of a batch
 // of tokens in two to five launches, with no host synchronisation (one token:
 // gate/up and down only, routed directly; the routing kernel from 2 tokens,
-// the input rotation pass from 8, the separate combine above 16).
+// the input rotation pass from 8, the separate combine above 48).
 //
 //   route    one workgroup groups the (token, slot) entries by expert on the
 //            device: active expert list, per-expert row counts/offsets and the
