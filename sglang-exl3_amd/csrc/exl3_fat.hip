@@ -194,6 +194,24 @@ bool fat_handoff(const FatPlan& pl, int m, int n) {
            (size_t)(n / 128) * (size_t)((m + pl.mt - 1) / pl.mt) <= kWsMaxCounters && fat_handoff_on();
 }
 
+// Rows from which a 16-row tile's split hand-off goes to a finish launch
+// (split_out; env EXL3_FAT_SPLIT_OUT=0: never).
+constexpr int kSplitOutMinRows = 6;
+
+// The second launch of a split-out hand-off: one wave per (row, column block).
+int fat_split_finish(const FatParams& p, int splits, hipStream_t st, const char* what) {
+    const unsigned wgs = (unsigned)(((long long)(p.n / 128) * p.M + 3) / 4);
+    const bool raw = p.rowsum != nullptr;
+    if (p.gu) {
+        if (raw) fat_split_finish_kernel<true, true><<<wgs, 256, 0, st>>>(p, splits);
+        else fat_split_finish_kernel<false, true><<<wgs, 256, 0, st>>>(p, splits);
+    } else {
+        if (raw) fat_split_finish_kernel<true, false><<<wgs, 256, 0, st>>>(p, splits);
+        else fat_split_finish_kernel<false, false><<<wgs, 256, 0, st>>>(p, splits);
+    }
+    return launch_status(what);
+}
+
 // tail: tail-split tiles (unsplit wide launch with fp16 output; 0 = none),
 // their hand-off tiles at tail_part and counts / flags at tail_sync.
 // rowsum: chunk sums of a's rows, [M][k/128], for a raw-entry plan (else null).
@@ -244,7 +262,13 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
         const int rc = launch_status("exl3 fat gemm zero fill");
         if (rc) return rc;
     }
-    return fat_launch(K, cb, pl.mt, p, pl.splits, st);
+    // the split-out finish of the gate/up path, on the plain hand-off
+    const bool split_out = p.handoff && pl.mt == 16 && M >= kSplitOutMinRows && pl.splits <= 4 &&
+                           env_int("EXL3_FAT_SPLIT_OUT", 1) != 0;
+    p.split_out = split_out ? 1 : 0;
+    const int rc = fat_launch(K, cb, pl.mt, p, pl.splits, st);
+    if (rc || !split_out) return rc;
+    return fat_split_finish(p, pl.splits, st, "exl3 fat gemm finish launch");
 }
 
 }  // namespace
@@ -401,7 +425,20 @@ int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate
             p.status = p.counters + kWsStatusIndex;
         }
     }
-    return fat_launch(K, cb, pl.mt, p, pl.splits, st);
+    // One 16-row tile of 6 to 16 rows with up to 4 k-splits: the splits store
+    // their partial tiles and exit, and fat_split_finish_kernel finishes every
+    // (row, column block) in a launch of its own (env EXL3_FAT_SPLIT_OUT=0:
+    // the in-kernel hand-off; same bits).  Config 3, graph-timed, in-kernel
+    // hand-off -> finish launch: M = 4 / 6 / 8 / 10 / 12 / 14 / 16: 22.90 /
+    // 24.48 / 24.95 / 26.1 / 26.21 / 27.1 / 27.22 -> 23.25 / 24.20 / 24.75 /
+    // 25.07 / 25.45 / 25.8 / 26.1 us (with four rows the last arrival's chain
+    // is short and the extra boundary does not pay).
+    const bool split_out = pl.mt == 16 && m >= kSplitOutMinRows && pl.splits <= 4 &&
+                           env_int("EXL3_FAT_SPLIT_OUT", 1) != 0;
+    p.split_out = split_out ? 1 : 0;
+    rc = fat_launch(K, cb, pl.mt, p, pl.splits, st);
+    if (rc || !split_out) return rc;
+    return fat_split_finish(p, pl.splits, st, "exl3_gate_up_swiglu finish launch");
 }
 
 }  // namespace exl3

@@ -270,6 +270,28 @@ def test_gemm_split_handoff_repeatable(m, cb, monkeypatch):
     check_close(outs[0].float().cpu().numpy(), atomic.float().cpu().numpy(), f"hand-off vs atomics m={m}")
 
 
+@pytest.mark.parametrize("m,cb", [(6, 2), (9, 1), (13, 0), (16, 2)])
+def test_gemm_split_out_finish_matches_in_kernel_handoff(m, cb, monkeypatch):
+    """From 6 to 16 rows exl3_gemm's narrow k-splits store their partial tiles
+    and a second launch (fat_split_finish_kernel) finishes every row; its sums
+    and epilogue are the in-kernel hand-off's, so both give the same bits
+    (EXL3_FAT_SPLIT_OUT=0 keeps the hand-off), mul1 raw entries included."""
+    k, n, K = 2048, 384, 3
+    print(f"case: gemm split-out finish m={m} cb={cb}", flush=True)
+    monkeypatch.setenv("EXL3_GEMM_GEMV_ROWS", "0")  # the MFMA path at every m
+    x = torch.from_numpy(make_x(m, k, seed=81 + m)).cuda()
+    tr, su, sv = make_weight(k, n, K, seed=82 + cb)
+    d = [torch.from_numpy(v).cuda() for v in (tr, su, sv)]
+    run = lambda: torch.ops.sglang_exl3.exl3_linear(x, *d, K, cb)
+    split = run()
+    monkeypatch.setenv("EXL3_FAT_SPLIT_OUT", "0")
+    handoff = run()
+    torch.cuda.synchronize()
+    assert torch.equal(split.view(torch.int16), handoff.view(torch.int16))
+    ref = oracle.matmul(x.cpu().numpy(), oracle.dequant(tr, su, sv, K, cb, rtz=True))
+    check_close(split.float().cpu().numpy(), ref, f"split-out m={m} cb={cb}")
+
+
 @pytest.mark.parametrize("m", [13, 40, 100, 250])
 @pytest.mark.parametrize("cb", [0, 1, 2])
 def test_gemm_split_handoff_ragged_rows(m, cb):

@@ -3,8 +3,8 @@ oracle: out = silu(min(x W_g, L)) * clamp(x W_u, -L, L), both weights sharing
 the input rotation suh, as the reference's fused gate/up path does
 (src/sglang_exl3/exl3.py:1184-1206).  Up to 3 rows the GEMV kernel (gate and
 up rounded to fp16 first), up to 160 the narrow MFMA kernel in gate/up mode
-(k-splits hand partial tiles to the last split), above the wide-tile MFMA
-kernel (fp32 accumulators throughout).  Bar: max-abs-err <= 2e-2 * rms(ref),
+(k-splits hand partial tiles to the last split, or up to 16 rows to a finish
+launch), above the wide-tile MFMA kernel (fp32 accumulators throughout).  Bar: max-abs-err <= 2e-2 * rms(ref),
 cosine >= 0.9999."""
 
 import numpy as np
@@ -75,6 +75,26 @@ def test_gate_up_split_handoff_ragged_rows(m, cb):
     assert torch.equal(first, again), "gate/up split hand-off: repeated calls differ"
     check_close(first.float().cpu().numpy(), _ref(x, tg, su, sg, tu, sv_u, K, cb, float("inf")),
                 f"gate_up split hand-off m={m} cb={cb}")
+
+
+@pytest.mark.parametrize("m,cb,limit", [(6, 2, 0.0), (9, 1, 1.5), (16, 2, 0.0), (16, 0, 2.0)])
+def test_gate_up_split_out_finish_matches_in_kernel_handoff(m, cb, limit, monkeypatch):
+    """From 6 to 16 rows the narrow gate/up k-splits store their partial tiles and
+    a second launch (fat_gu_finish_kernel) finishes every row; its sums and
+    epilogue are the in-kernel hand-off's, so both give the same bits
+    (EXL3_FAT_SPLIT_OUT=0 keeps the hand-off), also with a clamp and the
+    mul1 raw-entry map (cb 2)."""
+    k, n, K = 2048, 384, 3
+    print(f"case: gate_up split-out finish m={m} cb={cb} limit={limit}", flush=True)
+    tg, su, sg, tu, sv_u = _pair(k, n, K, seed=120 + m + cb)
+    x = make_x(m, k, seed=121 + m)
+    monkeypatch.setenv("EXL3_GATE_UP_GEMV_ROWS", "0")  # the MFMA path at every m
+    split = _run(x, tg, su, sg, tu, sv_u, K, cb, limit)
+    monkeypatch.setenv("EXL3_FAT_SPLIT_OUT", "0")
+    handoff = _run(x, tg, su, sg, tu, sv_u, K, cb, limit)
+    assert torch.equal(split.view(torch.int16), handoff.view(torch.int16))
+    ref = _ref(x, tg, su, sg, tu, sv_u, K, cb, limit if limit > 0 else float("inf"))
+    check_close(split.float().cpu().numpy(), ref, f"gate_up split-out m={m} cb={cb}")
 
 
 @pytest.mark.parametrize("m", [8, 200])
