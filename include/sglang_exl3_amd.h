@@ -193,7 +193,8 @@ size_t exl3_gate_up_workspace_size(int m, int k, int n, int K);
  * the input is rotated once and an MFMA kernel computes both projections of
  * a column block and applies the SwiGLU in its epilogue (g and u in fp32):
  * up to 160 rows the narrow kernel in gate/up mode (its k-splits hand fp32
- * partial tiles to the last split of each column block and row tile), above
+ * partial tiles to the last split of each column block and row tile, or,
+ * from 6 to 16 rows, to a finish launch that completes every row), above
  * it the wide-tile kernel, one workgroup holding the gate and up columns.  Replaces the gate/up half of
  * apply_exl3_batched_fat (src/sglang_exl3/exl3.py:1154-1206). */
 int exl3_gate_up_swiglu(const uint16_t* x, const uint16_t* suh, const int16_t* gate_trellis,
