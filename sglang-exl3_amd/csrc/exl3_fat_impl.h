@@ -956,24 +956,29 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
             const int c0 = bx * 128 + col;
             const EXL3_GLOBAL uint32_t* sgp = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh) + c0);
             const EXL3_GLOBAL uint32_t* sup = reinterpret_cast<const EXL3_GLOBAL uint32_t*>(gptr(p.svh2) + c0);
-            const bool clamp = p.limit > 0.0f && p.limit < __builtin_huge_valf();
-            uint32_t ow[8];
 #pragma unroll
             for (int e2 = 0; e2 < 8; ++e2) {
                 const uint32_t sgw = sgp[e2], suw = sup[e2];
-                float r[2];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int e = 2 * e2 + h;
-                    float gg = (gv[e] * hn) * __half2float(__ushort_as_half((unsigned short)(sgw >> (16 * h))));
-                    float uu = (uv[e] * hn) * __half2float(__ushort_as_half((unsigned short)(suw >> (16 * h))));
-                    if (clamp) {
-                        gg = fminf(gg, p.limit);
-                        uu = fminf(fmaxf(uu, -p.limit), p.limit);
-                    }
-                    r[h] = silu_f(gg) * uu;
+                    gv[e] = (gv[e] * hn) * __half2float(__ushort_as_half((unsigned short)(sgw >> (16 * h))));
+                    uv[e] = (uv[e] * hn) * __half2float(__ushort_as_half((unsigned short)(suw >> (16 * h))));
                 }
-                const __half2 o = h2_rn(r[0], r[1]);
+            }
+            // one uniform branch around all 32 values: a per-value test is
+            // turned into selects that cost 80 VALU per pass without a clamp
+            if (p.limit > 0.0f && p.limit < __builtin_huge_valf()) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    gv[e] = fminf(gv[e], p.limit);
+                    uv[e] = fminf(fmaxf(uv[e], -p.limit), p.limit);
+                }
+            }
+            uint32_t ow[8];
+#pragma unroll
+            for (int e2 = 0; e2 < 8; ++e2) {
+                const __half2 o = h2_rn(silu_f(gv[2 * e2]) * uv[2 * e2], silu_f(gv[2 * e2 + 1]) * uv[2 * e2 + 1]);
                 ow[e2] = *reinterpret_cast<const uint32_t*>(&o);
             }
             if (trow < rows) {
