@@ -177,13 +177,20 @@ int check_fat(const char* fn, const void* a, const void* trellis, const void* ou
     return EXL3_OK;
 }
 
-// Narrow 16-row tiles on mul1 weights read the raw entries (two VALU ops per
-// two weights instead of four) and correct in the epilogue from the rotated
-// rows' chunk sums.  Graph-timed, raw / decoded: config 3 gate/up M = 16:
-// 29.3 / 31.6 us, exl3_gemm k = 4096, n = 14336, M = 16: 22.7 / 23.2 us; on
-// 64-row tiles the per-row sums cost more than the decode saves (gate/up
-// M = 64: 55.8 / 53.7 us).  EXL3_FAT_RAW=0 turns it off (ablation).
-bool fat_raw(int cb, int mt) { return cb == 2 && mt == 16 && env_int("EXL3_FAT_RAW", 1) != 0; }
+// Narrow 16-row tiles and wide tiles on mul1 weights read the raw entries
+// (two VALU ops per two weights instead of four) and correct in the epilogue
+// from the rotated rows' chunk sums.  Graph-timed, raw / decoded: config 3
+// gate/up M = 16: 29.3 / 31.6 us, exl3_gemm k = 4096, n = 14336, M = 16:
+// 22.7 / 23.2 us; on 64-row tiles the per-row sums cost more than the
+// decode saves (gate/up M = 64: 55.8 / 53.7 us).  Wide tiles in gate/up mode
+// sum a row's chunks in the epilogue, on the row's 8 lanes (config 3 M = 256
+// / 2048: 89.4 / 478.9 -> 87.7 / 467.6 us); plain wide tiles stay decoded
+// (exl3_gemm K = 3 mul1, n = 14336, M = 256 / 2048: 69.9 / 250.9 -> 70.3 /
+// 250.3 us, each row's sums taken once per 128-column block).
+// EXL3_FAT_RAW=0 turns it off (ablation).
+bool fat_raw(int cb, int mt, bool gu) {
+    return cb == 2 && (mt == 16 || (mt == FAT_MT_WIDE && gu)) && env_int("EXL3_FAT_RAW", 1) != 0;
+}
 
 // Narrow plans with k-splits and fp16 output hand partial tiles to the last
 // split of each (column block, row tile) instead of adding fp32 atomically
@@ -228,7 +235,7 @@ int run_fat(const uint16_t* a, const int16_t* trellis, float* out32, __half* out
         p.partials = partials;
         p.counters = counters;
     }
-    if (rowsum && fat_raw(cb, pl.mt)) p.rowsum = rowsum;
+    if (rowsum && fat_raw(cb, pl.mt, false)) p.rowsum = rowsum;
     if (tail > 0) {
         p.tiles_x = n / FB_COLS;
         p.tail_tiles = tail;
@@ -300,7 +307,7 @@ int fat_gemm_rows(const uint16_t* x, const int16_t* trellis, const uint16_t* suh
     __half* xr = reinterpret_cast<__half*>(reinterpret_cast<char*>(ws) + kWsScratchOffset);
     float* o32 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kWsScratchOffset + fat_xr_bytes(m, k));
     const FatPlan pl = plan_fat(m, k, n, true);
-    float* rs = fat_raw(cb, pl.mt)
+    float* rs = fat_raw(cb, pl.mt, false)
                     ? reinterpret_cast<float*>(reinterpret_cast<char*>(xr) + fat_xr_only_bytes(m, k))
                     : nullptr;
     const long long chunks = (long long)m * (k / 128);
@@ -390,7 +397,7 @@ int fat_gate_up_rows(const uint16_t* x, const uint16_t* suh, const int16_t* gate
                       "exl3_gate_up_swiglu: %d column blocks exceed the workspace counters", n / 128);
     char* w8 = reinterpret_cast<char*>(ws);
     __half* xr = reinterpret_cast<__half*>(w8 + kWsScratchOffset);
-    float* rs = fat_raw(cb, pl.mt) ? reinterpret_cast<float*>(w8 + kWsScratchOffset + fat_xr_only_bytes(m, k)) : nullptr;
+    float* rs = fat_raw(cb, pl.mt, true) ? reinterpret_cast<float*>(w8 + kWsScratchOffset + fat_xr_only_bytes(m, k)) : nullptr;
     const long long chunks = (long long)m * (k / 128);
     rotate_rows_kernel<<<(unsigned)((chunks + 3) / 4), 256, 0, st>>>(reinterpret_cast<const __half*>(x),
                                                                       reinterpret_cast<const __half*>(suh), xr, chunks,

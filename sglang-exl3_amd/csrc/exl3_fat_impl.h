@@ -626,30 +626,36 @@ constexpr size_t fat_big_smem_bytes() {
     return stage > tile ? stage : tile;
 }
 
-// fp16 pair of tile rows (4H + kofs(2P), +1) of column q + 8C (round to nearest).
-template <int K, int CB, int H, int C, int P>
+// fp16 pair of tile rows (4H + kofs(2P), +1) of column q + 8C (round to
+// nearest; RAW: the mul1 raw entries of mul1_raw_pair).
+template <int K, int CB, int H, int C, int P, bool RAW = false>
 __device__ __forceinline__ uint32_t nat_pair(const uint32_t* buf, const uint32_t* mid) {
     constexpr int e0 = 2 * P, e1 = 2 * P + 1;
     constexpr int u0 = 16 * H + (e0 & 3) + 8 * (e0 >> 2) + 4 * C;
     constexpr int u1 = 16 * H + (e1 & 3) + 8 * (e1 >> 2) + 4 * C;
-    return decode2_rn<CB>(window_mid<K, u0>(buf, mid), window_mid<K, u1>(buf, mid));
+    if constexpr (RAW) {
+        static_assert(CB == 2, "raw entries: mul1");
+        return mul1_raw_pair(window_mid<K, u0>(buf, mid), window_mid<K, u1>(buf, mid));
+    } else {
+        return decode2_rn<CB>(window_mid<K, u0>(buf, mid), window_mid<K, u1>(buf, mid));
+    }
 }
 
 // f[h'][j] = tile rows (8h' + 2j, +1) of column q + 8C: run H = j >> 1, pair P = h' + 2 (j & 1).
-template <int K, int CB, int C>
+template <int K, int CB, int C, bool RAW>
 __device__ __forceinline__ void nat_column(const uint32_t* buf, const uint32_t* mid, uint32_t (&f)[2][4]) {
-    f[0][0] = nat_pair<K, CB, 0, C, 0>(buf, mid);
-    f[0][1] = nat_pair<K, CB, 0, C, 2>(buf, mid);
-    f[0][2] = nat_pair<K, CB, 1, C, 0>(buf, mid);
-    f[0][3] = nat_pair<K, CB, 1, C, 2>(buf, mid);
-    f[1][0] = nat_pair<K, CB, 0, C, 1>(buf, mid);
-    f[1][1] = nat_pair<K, CB, 0, C, 3>(buf, mid);
-    f[1][2] = nat_pair<K, CB, 1, C, 1>(buf, mid);
-    f[1][3] = nat_pair<K, CB, 1, C, 3>(buf, mid);
+    f[0][0] = nat_pair<K, CB, 0, C, 0, RAW>(buf, mid);
+    f[0][1] = nat_pair<K, CB, 0, C, 2, RAW>(buf, mid);
+    f[0][2] = nat_pair<K, CB, 1, C, 0, RAW>(buf, mid);
+    f[0][3] = nat_pair<K, CB, 1, C, 2, RAW>(buf, mid);
+    f[1][0] = nat_pair<K, CB, 0, C, 1, RAW>(buf, mid);
+    f[1][1] = nat_pair<K, CB, 0, C, 3, RAW>(buf, mid);
+    f[1][2] = nat_pair<K, CB, 1, C, 1, RAW>(buf, mid);
+    f[1][3] = nat_pair<K, CB, 1, C, 3, RAW>(buf, mid);
 }
 
 // Decode one 32-value group (words w[0..K-1], previous word from lane q - 1).
-template <int K, int CB>
+template <int K, int CB, bool RAW = false>
 __device__ __forceinline__ void nat_group(const uint32_t (&w)[K], int prev_addr, uint32_t (&f)[2][2][4]) {
     uint32_t buf[K + 1], mid[K];
 #pragma unroll
@@ -657,8 +663,26 @@ __device__ __forceinline__ void nat_group(const uint32_t (&w)[K], int prev_addr,
     buf[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(prev_addr, (int)buf[K]);
 #pragma unroll
     for (int j = 0; j < K; ++j) mid[j] = __builtin_amdgcn_alignbit(buf[j], buf[j + 1], 16);
-    nat_column<K, CB, 0>(buf, mid, f[0]);
-    nat_column<K, CB, 1>(buf, mid, f[1]);
+    nat_column<K, CB, 0, RAW>(buf, mid, f[0]);
+    nat_column<K, CB, 1, RAW>(buf, mid, f[1]);
+}
+
+// mul1 raw entries in the x16 layout (a tile row on 8 lanes, 16 columns
+// each): kMul1Bias * S, S the sum of the row's x over chunks [c0, c0 + nc)
+// of rowsum (lane j of the 8 adds chunks j, j + 8, .., then the 8 partials
+// meet by DPP), and the correction v = v * kMul1Kinv + that term.
+__device__ __forceinline__ float raw_row_bias(const FatParams& p, int row, int c0, int nc, int lane) {
+    const float* r = p.rowsum + (size_t)row * (p.k >> 7) + c0;
+    float t = 0.f;
+    for (int c = lane & 7; c < nc; c += 8) t += gptr(r)[c];
+    t += lane_xor<1>(t);
+    t += lane_xor<2>(t);
+    t += lane_xor<4>(t);
+    return kMul1Bias * t;
+}
+__device__ __forceinline__ void raw_fix16(float (&v)[16], float sx) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = v[e] * kMul1Kinv + sx;
 }
 
 // GU = true: gate/up mode.  Workgroup bx then covers column block bx of both
@@ -668,7 +692,11 @@ __device__ __forceinline__ void nat_group(const uint32_t (&w)[K], int prev_addr,
 // in registers.  The reference's fused path concatenates the two packs per
 // call and combines them with separate torch kernels
 // (src/sglang_exl3/exl3.py:1184-1206).
-template <int K, int CB, bool GU>
+// RAW (mul1, p.rowsum set): B holds the raw entries (mul1_raw_pair) and the
+// epilogue applies kMul1Kinv * acc + kMul1Bias * (the row's x sum over the
+// k range) before the output rotation, two VALU per pair of states fewer in
+// the decode (config 3 M = 2048, whole-tile harness: 497.6 -> 483.2 us).
+template <int K, int CB, bool GU, bool RAW = false>
 __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
     constexpr int RB = FB_ROWS / 2 / 16;  // row blocks per wave
     static_assert(FB_A_BYTES == 4 * 16 * FB_THREADS, "four 16-byte A chunks per thread and step");
@@ -752,7 +780,7 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
     auto load_step = [&](int step) { load_words<K>(tb + (size_t)step * step_stride, w); };
     auto decode_post = [&](int bufi) {
         uint32_t fr[2][2][4];  // [column half][h'][j]
-        nat_group<K, CB>(w, prev_addr, fr);
+        nat_group<K, CB, RAW>(w, prev_addr, fr);
         unsigned char* bb = bsm + (size_t)bufi * FB_B_BYTES;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
@@ -950,6 +978,12 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
                 gv[4 * q4] = a.x; gv[4 * q4 + 1] = a.y; gv[4 * q4 + 2] = a.z; gv[4 * q4 + 3] = a.w;
                 uv[4 * q4] = b.x; uv[4 * q4 + 1] = b.y; uv[4 * q4 + 2] = b.z; uv[4 * q4 + 3] = b.w;
             }
+            if constexpr (RAW) {
+                const float sx = raw_row_bias(p, m0 + (trow < rows ? trow : rows - 1), sidx * (p.ksteps >> 1),
+                                              p.ksteps >> 1, lane);
+                raw_fix16(gv, sx);
+                raw_fix16(uv, sx);
+            }
             fwht128_x16(gv, lane);
             fwht128_x16(uv, lane);
             const float hn = fwht_x16_norm(lane);
@@ -1005,6 +1039,9 @@ __global__ __launch_bounds__(FB_THREADS, 2) void fat_big_kernel(FatParams p) {
                 v[4 * q + 2] = t.z;
                 v[4 * q + 3] = t.w;
             }
+            if constexpr (RAW)
+                raw_fix16(v, raw_row_bias(p, m0 + (trow < rows ? trow : rows - 1), sidx * (p.ksteps >> 1),
+                                          p.ksteps >> 1, lane));
             fwht128_x16(v, lane);
             const float hn = fwht_x16_norm(lane);
             const int c0 = bx * FB_COLS + col;
@@ -1069,16 +1106,17 @@ int fat_launch_k(int cb, int mt, const FatParams& p, int splits, hipStream_t st)
         dim3 grid(p.gu ? p.n / 128 : p.n / FB_COLS, (p.M + FB_ROWS - 1) / FB_ROWS, splits);
         if (p.tail_tiles > 0) grid = dim3(p.tail_first + 2 * p.tail_tiles, 1, 1);
         const size_t smem = fat_big_smem_bytes();
-#define EXL3_FATB(CBV, GUV)                                                                            \
-    if (cb == CBV && (p.gu != 0) == GUV) {                                                             \
-        const void* fn = reinterpret_cast<const void*>(&fat_big_kernel<K, CBV, GUV>);                  \
+#define EXL3_FATB(CBV, GUV, RAWV)                                                                      \
+    if (cb == CBV && (p.gu != 0) == GUV && (p.rowsum != nullptr) == RAWV) {                            \
+        const void* fn = reinterpret_cast<const void*>(&fat_big_kernel<K, CBV, GUV, RAWV>);            \
         const int lrc = allow_dynamic_lds(fn, smem, "exl3 fat gemm (wide tiles)");                     \
         if (lrc) return lrc;                                                                           \
-        fat_big_kernel<K, CBV, GUV><<<grid, FB_THREADS, smem, st>>>(p);                                \
+        fat_big_kernel<K, CBV, GUV, RAWV><<<grid, FB_THREADS, smem, st>>>(p);                          \
         return launch_status("exl3 fat gemm launch");                                                  \
     }
-        EXL3_FATB(0, false) EXL3_FATB(1, false) EXL3_FATB(2, false)
-        EXL3_FATB(0, true) EXL3_FATB(1, true) EXL3_FATB(2, true)
+        EXL3_FATB(0, false, false) EXL3_FATB(1, false, false) EXL3_FATB(2, false, false)
+        EXL3_FATB(0, true, false) EXL3_FATB(1, true, false) EXL3_FATB(2, true, false)
+        EXL3_FATB(2, true, true)
 #undef EXL3_FATB
     }
     dim3 grid((p.gu ? 2 : 1) * (p.n / 128), (p.M + mt - 1) / mt, splits);

@@ -213,10 +213,11 @@ def test_mul1_raw_entries(op, m, monkeypatch):
     sum, no affine step) and correct in the epilogue with kinv * acc + bias *
     (row sum of the rotated x over the split's k range).  k = 14336 (112 chunk
     sums per row), 16-row tiles with k-splits (m = 16): against the oracle and
-    close to the decoded path (EXL3_FAT_RAW=0).  The 64-row tiles (m = 48) and
-    the wide tiles (gemm m = 300, forced by EXL3_FAT_WIDE=2: 16 fp32-atomic
-    k-splits; gate/up m = 200: tail-split k-halves) decode values and are
-    checked at the same k."""
+    close to the decoded path (EXL3_FAT_RAW=0).  The wide tiles in gate/up mode
+    (m = 200: tail-split k-halves, the row sums taken in the epilogue) read
+    raw entries too; the 64-row tiles (m = 48) and the plain wide tiles (gemm
+    m = 300, forced by EXL3_FAT_WIDE=2: 16 fp32-atomic k-splits) decode values
+    and are checked at the same k."""
     k, n, K, cb = 14336, 256, 3, 2
     if op == "gemm" and m > 256:
         monkeypatch.setenv("EXL3_FAT_WIDE", "2")
