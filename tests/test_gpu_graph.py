@@ -4,7 +4,8 @@ pack; here with valid packs).
 
 One graph holds exl3_gemv (balanced kernel at m=1, k-split kernel at m=4),
 exl3_gemm (MFMA path at m=100), exl3_linear (3INST), dequant_trellis,
-p2b_gemv_batched, exl3_gate_up_swiglu (GEMV and MFMA paths), exl3_fat_gemm and
+p2b_gemv_batched, exl3_gate_up_swiglu (GEMV, narrow MFMA with and without the
+split-out finish launch, wide tiles on mul1 raw entries), exl3_fat_gemm and
 exl3_fat_gemm_scatter.  It is replayed several times, with new inputs copied
 into the captured input tensors and eager calls of the same ops on the same
 stream between replays; every replay must equal the eager result on the same
@@ -44,7 +45,7 @@ def test_dense_ops_graph_capture_replay():
     tok = torch.randperm(64, generator=torch.Generator().manual_seed(0))[:48].cuda()
     rw = (torch.rand(48, generator=torch.Generator().manual_seed(1)) + 0.5).to(torch.float16).cuda()
 
-    xs = {m: torch.zeros((m, k), dtype=torch.float16, device="cuda") for m in (1, 2, 4, 48, 100)}
+    xs = {m: torch.zeros((m, k), dtype=torch.float16, device="cuda") for m in (1, 2, 4, 16, 48, 100, 200)}
     fat_out = torch.zeros((48, n), dtype=torch.float32, device="cuda")
     scat_out = torch.zeros((64, n), dtype=torch.float32, device="cuda")
 
@@ -58,6 +59,9 @@ def test_dense_ops_graph_capture_replay():
         o["batched"] = torch.ops.sglang_exl3.p2b_gemv_batched(xs[2], *tabs, ids, K, True, n)
         o["gu2"] = torch.ops.sglang_exl3.exl3_gate_up_swiglu(xs[2], su, trg, svg, tru, svu, K, 1)
         o["gu100"] = torch.ops.sglang_exl3.exl3_gate_up_swiglu(xs[100], su, trg, svg, tru, svu, K, 2, 4.0)
+        # 16 rows: the split-out finish launch; 200 rows: wide tiles with mul1 raw entries
+        o["gu16"] = torch.ops.sglang_exl3.exl3_gate_up_swiglu(xs[16], su, trg, svg, tru, svu, K, 2)
+        o["gu200"] = torch.ops.sglang_exl3.exl3_gate_up_swiglu(xs[200], su, trg, svg, tru, svu, K, 2)
         fat_out.zero_()
         torch.ops.sglang_exl3.exl3_fat_gemm(xs[48], tr, fat_out, sv, K, True, False)
         scat_out.zero_()
