@@ -416,6 +416,7 @@ constexpr int kMoeGfxTokens = 3;  // routed batches with the split fixed-point g
 struct MoeLayout {
     int entries, max_units;
     bool rot, fc;
+    bool fr;  // the one-launch gate/up + down pass may run (its own down partials)
     MoePlan gu, dn;
     size_t route_off, units_off, rows_off, tokv_off, h_off, y_off, xr_off, part_off, part_dn_off, total;
 };
@@ -443,8 +444,12 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     // threshold (0: never fused).
     const int fc_tokens = env_int("EXL3_MOE_FC_TOKENS", kMoeFusedCombineTokens);
     L.fc = tokens <= fc_tokens && (size_t)tokens * hidden * 8 <= kWsAccBytes && topk <= SK_MAX_CONTRIB;
+    // the one-launch gate/up + down pass (env EXL3_MOE_FUSED_ROUTED=1) keeps
+    // the down items short: 12-step items would hold the launch's LDS (the
+    // larger of the two passes') at two workgroups per CU
+    L.fr = tokens > 1 && env_int("EXL3_MOE_FUSED_ROUTED", 0) != 0;
     L.gu = plan_moe(units, L.entries, hidden, inter, 2, 1536.0);
-    L.dn = plan_moe(units, L.entries, inter, hidden, 1, L.fc ? 700.0 : 1536.0);
+    L.dn = plan_moe(units, L.entries, inter, hidden, 1, L.fr ? 1e30 : (L.fc ? 700.0 : 1536.0));
     size_t o = kWsScratchOffset;
     L.route_off = o;
     o = align256(o + 4 * sizeof(int));
@@ -464,14 +469,16 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     L.xr_off = o;
     if (L.rot) o = align256(o + (size_t)2 * L.entries * hidden * 2);
     // split partials: one region that the gate/up and down launches reuse in
-    // turn; one token gets a second one for the down items, which run
-    // alongside the gate/up items in the fused one-token launch
+    // turn; one token, and routed batches with the one-launch gate/up + down
+    // pass (env EXL3_MOE_FUSED_ROUTED=1), get a second one for the down items,
+    // which then run alongside the gate/up items
+    const bool two = tokens == 1 || L.fr;
     L.part_off = o;
     const size_t pg = (size_t)(inter / 128) * 2 * L.gu.splits;
     const size_t pd = (size_t)(hidden / 128) * 1 * L.dn.splits;
-    o = align256(o + (tokens == 1 ? pg : (pg > pd ? pg : pd)) * L.entries * 128 * sizeof(float));
-    L.part_dn_off = tokens == 1 ? o : L.part_off;
-    if (tokens == 1) o = align256(o + pd * L.entries * 128 * sizeof(float));
+    o = align256(o + (two ? pg : (pg > pd ? pg : pd)) * L.entries * 128 * sizeof(float));
+    L.part_dn_off = two ? o : L.part_off;
+    if (two) o = align256(o + pd * L.entries * 128 * sizeof(float));
     L.total = o;
     return L;
 }
@@ -583,6 +590,15 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
                      env_int("EXL3_MOE_GFX", 1) != 0;
     const int gu_ns = gfx ? gfx_ns : L.gu.ns;
     const bool fused = fuse_req && moe_fused_steps_ok(gu_ns);
+    // Routed batch, gate/up and down in one launch after the routing launch
+    // (moe_fused_routed_kernel; opt-in, env EXL3_MOE_FUSED_ROUTED=1): counters
+    // [gate/up hand-off | down hand-off | readiness counts | done counts] per
+    // work unit in the zeroed counter region
+    const size_t fr_units = (size_t)L.max_units;
+    const size_t fr_ready = (fr_units * (inter / 128 + hidden / 128) + 255) & ~(size_t)255;
+    const bool fused_routed = L.fr && !direct && L.rot && KG == KU && KU == KD && L.gu.kw == 1 && L.dn.kw == 1 &&
+                              moe_fused_routed_steps_ok(gu_ns, L.dn.ns, gfx, dn_fxs) &&
+                              fr_ready + fr_units * (ready_stride + 1) <= kWsMaxCounters;
     unsigned long long* const acc_base = reinterpret_cast<unsigned long long*>(w8 + kWsAccOffset);
 
     // 3. gate + up (+ SwiGLU + down input rotation; GFX: the gate and up rows)
@@ -614,6 +630,18 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
         pg.max_polls = wait_polls();
         pg.status = c0 + kWsStatusIndex;
         pg.ready_nblk = nbg;
+        pg.ready_stride = ready_stride;
+        pg.ready_target = gfx ? 2 * pg.splits : 1;
+        pg.poll_sleep = env_int("EXL3_MOE_POLL_SLEEP", 1);
+        pg.prime_late = env_int("EXL3_MOE_PRIME_LATE", 0);
+    } else if (fused_routed) {
+        int* c0 = reinterpret_cast<int*>(w8);
+        pg.ready = c0 + fr_ready;
+        pg.done = pg.ready + fr_units * ready_stride;
+        pg.ticket = nullptr;
+        pg.max_polls = wait_polls();
+        pg.status = c0 + kWsStatusIndex;
+        pg.ready_nblk = inter / 128;
         pg.ready_stride = ready_stride;
         pg.ready_target = gfx ? 2 * pg.splits : 1;
         pg.poll_sleep = env_int("EXL3_MOE_POLL_SLEEP", 1);
@@ -653,8 +681,8 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.weights_f16 = weights_f16;
     p.final_out = reinterpret_cast<__half*>(out);
     p.fxs = dn_fxs;
-    if (fused) {
-        p.counters = reinterpret_cast<int*>(w8) + (size_t)topk * (inter / 128);
+    if (fused || fused_routed) {
+        p.counters = reinterpret_cast<int*>(w8) + (fused ? (size_t)topk : fr_units) * (inter / 128);
         p.partials = reinterpret_cast<float*>(w8 + L.part_dn_off);
         p.ready = pg.ready;
         p.done = pg.done;

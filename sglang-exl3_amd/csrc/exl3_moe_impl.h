@@ -1,7 +1,9 @@
 // Batched routed-expert MoE layer for gfx950: every active expert of a batch
 // of tokens in two to five launches, with no host synchronisation (one token:
-// gate/up and down only, routed directly; the routing kernel from 2 tokens,
-// the input rotation pass from 8, the separate combine above 48).
+// gate/up and down only, routed directly; from 2 tokens the routing kernel,
+// which also rotates the gate/up inputs; the separate combine above 48).  Opt-in,
+// gate/up and down also run as one persistent launch (moe_fused_direct_kernel
+// for one token, moe_fused_routed_kernel after the routing launch).
 //
 //   route    one workgroup groups the (token, slot) entries by expert on the
 //            device: active expert list, per-expert row counts/offsets and the
@@ -853,6 +855,32 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
     }
 }
 
+// Routed batch, gate/up and down in one persistent launch over the active
+// units (after the routing launch, which also rotates the gate/up inputs).
+// Items [0, Ngu) are the gate/up items, [Ngu, Ngu + Ndn) the down items, taken
+// in the snake rounds of moe_gemv_kernel.  A gate/up item publishes its h
+// blocks (readiness counts per unit and 128-wide block, as in the one-token
+// launch); a down item requests its weights, then waits (bounded) for the
+// blocks of its k range.  Forward progress: every workgroup is resident (the
+// grid is the device's resident capacity), gate/up items never wait, and a
+// down item waits only for items of lower index, i.e. of its own round or an
+// earlier one, which the other resident workgroups reach without waiting on
+// anything later.  DFX: the down pass adds into the fused combine's
+// fixed-point accumulators (one round trip per split).
+template <int K, int CB, int NSG, int NSD, bool GFX, bool DFX>
+__global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_routed_kernel(MoeParams pg, MoeParams pd) {
+    extern __shared__ __align__(16) unsigned char mv_smem[];
+    static_assert(!GFX || DFX, "split fixed-point gate/up: the down pass stages the SwiGLU, FXS items");
+    const int nunits = uniform_i(gptr(pg.rt.counts)[1]);
+    const int ngu = nunits * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits;
+    const int total = ngu + nunits * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
+    const int G = gridDim.x, b0 = blockIdx.x;
+    for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0)) {
+        if (it < ngu) moe_item<K, CB, NSG, MV_GU_ROT, 1, true, GFX, GFX>(pg, it, mv_smem, 0, rnd == 0);
+        else moe_item<K, CB, NSD, MV_DOWN, 1, true, DFX, GFX>(pd, it - ngu, mv_smem, 0, rnd == 0);
+    }
+}
+
 // Dynamic LDS bytes of moe_gemv_kernel.
 // fxs: the split fixed-point down pass, whose one k-wave still meets in an
 // LDS tile of the unit's rows.
@@ -925,10 +953,43 @@ inline bool moe_gfx_steps_ok(int ns) { return ns == 2 || ns == 4 || ns == 8; }
 // Step counts the fused one-token kernel is instantiated for (per pass).
 inline bool moe_fused_steps_ok(int ns) { return ns == 2 || ns == 4 || ns == 8; }
 
+// Step counts the fused routed kernel is instantiated for: gate/up, down
+// (gfx: split fixed-point gate/up; dfx: split fixed-point down).
+inline bool moe_fused_routed_steps_ok(int nsg, int nsd, bool gfx, bool dfx) {
+    if (nsg != 8 || (gfx && !dfx)) return false;
+    return nsd == 4 || nsd == 8 || (nsd == 12 && !gfx);
+}
+
 template <int K>
 int moe_fused_launch_k(int cb, int nsg, int nsd, const MoeParams& pg, const MoeParams& pd, hipStream_t st) {
     const bool gfx = pg.gfx != 0;
     const size_t sg = moe_smem_bytes(4 * nsg, 1, gfx), sd = moe_smem_bytes(4 * nsd, 1, gfx);
+    if (!pg.direct) {
+        // routed batch: the item count is on the device, so the grid is the
+        // resident capacity and workgroups past the items exit at once
+        const bool dfx = pd.fxs != 0;
+        const size_t sdr = moe_smem_bytes(4 * nsd, 1, dfx);
+        const size_t smem = sg > sdr ? sg : sdr;
+#define EXL3_MFR(CBV, NG, ND, GFV, DFV)                                                                     \
+    if (cb == CBV && nsg == NG && nsd == ND && gfx == GFV && dfx == DFV) {                                 \
+        const void* fn = reinterpret_cast<const void*>(&moe_fused_routed_kernel<K, CBV, NG, ND, GFV, DFV>); \
+        const int lrc = allow_dynamic_lds(fn, smem, "exl3 moe fused routed");                              \
+        if (lrc) return lrc;                                                                               \
+        const int grid = moe_fused_grid_size(fn, smem);                                                    \
+        if (grid <= 0) return EXL3_ERR_HIP;                                                                \
+        moe_fused_routed_kernel<K, CBV, NG, ND, GFV, DFV><<<grid, 256, smem, st>>>(pg, pd);                \
+        return launch_status("exl3 moe fused routed launch");                                              \
+    }
+#define EXL3_MFR_CB(CBV)                                                                                     \
+    EXL3_MFR(CBV, 8, 8, false, false) EXL3_MFR(CBV, 8, 8, false, true) EXL3_MFR(CBV, 8, 12, false, false) \
+    EXL3_MFR(CBV, 8, 12, false, true) EXL3_MFR(CBV, 8, 8, true, true) EXL3_MFR(CBV, 8, 4, false, true)    \
+    EXL3_MFR(CBV, 8, 4, true, true) EXL3_MFR(CBV, 8, 4, false, false)
+        EXL3_MFR_CB(0) EXL3_MFR_CB(1) EXL3_MFR_CB(2)
+#undef EXL3_MFR_CB
+#undef EXL3_MFR
+        set_error("exl3 moe: no fused routed kernel for codebook %d steps %d / %d", cb, nsg, nsd);
+        return EXL3_ERR_UNSUPPORTED;
+    }
     const size_t smem = sg > sd ? sg : sd;
     const int items = pg.topk * ((pg.n >> 7) / pg.bx_per_item) * pg.proj_launch * pg.splits +
                       pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;

@@ -346,6 +346,72 @@ def test_moe_one_token_fused_split_fixed_point(E, hidden, inter, K, cb, topk, in
         check_close(o, ex.ref(x, ids, w), f"moe fused gfx one token E={E}")
 
 
+@pytest.mark.parametrize("T,topk,E,hidden,inter,K,cb,invalid", [
+    (2, 8, 128, 2048, 768, 3, 1, 0),      # split fixed-point gate/up, 4-step down items
+    (3, 4, 16, 512, 512, 2, 2, 1),        # mul1, 8-step down items
+    (16, 8, 128, 2048, 768, 3, 1, 0),     # headline shape: fused combine, 12-step down items
+    (16, 8, 32, 1024, 1536, 4, 0, 3),     # 3INST
+    (40, 2, 4, 512, 512, 3, 1, 2),        # more than 16 rows per expert: several units per expert
+    (64, 8, 128, 2048, 768, 3, 1, 0),     # separate combine, per-block hand-off of the down pass
+])
+def test_moe_routed_fused_launch(T, topk, E, hidden, inter, K, cb, invalid, monkeypatch):
+    """A routed batch with gate/up and down in one launch after the routing launch (opt-in,
+    EXL3_MOE_FUSED_ROUTED=1, which plans 4- or 8-step down items): same bits as the separate gate/up
+    and down launches with the same items, repeated calls agree (readiness counts, hand-off counters
+    and accumulators are left clear), and against the oracle."""
+    print(f"case: moe fused routed T={T} topk={topk} E={E} h={hidden} i={inter} K={K} cb={cb} invalid={invalid}",
+          flush=True)
+    monkeypatch.setenv("EXL3_MOE_DN_NSTEPS", "4" if inter % 512 else "8")  # the fused pass's down items
+    ex = Experts(E, hidden, inter, (K, K, K), cb, seed=230 + T + E)
+    x = make_x(T, hidden, seed=231 + T)
+    ids, w = _routing(T, topk, E, seed=232 + T, invalid=invalid)
+    outs = {}
+    for fused in ("0", "1", "1"):
+        monkeypatch.setenv("EXL3_MOE_FUSED_ROUTED", fused)
+        o = _layer_capi(ex, x, ids, w, cb=cb)
+        torch.cuda.synchronize()
+        if fused in outs:
+            assert torch.equal(o, outs[fused]), "repeated fused routed call differs"
+        outs[fused] = o
+    assert torch.equal(outs["0"], outs["1"]), "fused routed launch differs from the separate launches"
+    check_close(outs["1"].float().cpu().numpy(), ex.ref(x, ids, w), f"moe fused routed T={T}")
+
+
+def test_moe_routed_fused_graph(monkeypatch):
+    """The routed one-launch gate/up + down pass captured in a HIP graph: replays interleaved with
+    eager calls match the eager result, and a routing change between replays is picked up."""
+    monkeypatch.setenv("EXL3_MOE_FUSED_ROUTED", "1")
+    T, E, hidden, inter, topk = 12, 32, 512, 768, 8
+    ex = Experts(E, hidden, inter, (3, 3, 3), 1, seed=240)
+    x = make_x(T, hidden, seed=241)
+    ids, w = _routing(T, topk, E, seed=242)
+    xd, idd, wd = (torch.from_numpy(a).cuda() for a in (x, ids, w))
+    a = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gout = ex.layer(xd, idd, wd)
+    torch.cuda.synchronize()
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, a), f"graph replay {r} differs from eager"
+        ex.layer(xd, idd, wd)
+        torch.cuda.synchronize()
+    ids2, w2 = _routing(T, topk, E, seed=243, invalid=3)
+    idd.copy_(torch.from_numpy(ids2))
+    wd.copy_(torch.from_numpy(w2))
+    g.replay()
+    torch.cuda.synchronize()
+    check_close(gout.float().cpu().numpy(), ex.ref(x, ids2, w2), "moe fused routed graph new routing")
+
+
 def test_moe_one_token_fused_graph(monkeypatch):
     """The fused one-token launch captured in a HIP graph: replays interleaved with eager calls
     match the eager result, and a routing change between replays is picked up."""
