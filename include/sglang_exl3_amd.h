@@ -36,7 +36,7 @@ extern "C" {
 
 /* Bits of the workspace status word (exl3_workspace_status): a bounded wait
  * inside a launch gave up, so that launch's output is not valid. */
-#define EXL3_WAIT_MOE_FUSED 1 /* one-launch one-token MoE: a down item's wait for its h blocks */
+#define EXL3_WAIT_MOE_FUSED 1 /* one-launch MoE gate/up + down pass: a down item's wait for its h blocks */
 #define EXL3_WAIT_FAT_TAIL 2  /* wide-tile GEMM tail split: the second k-half's wait for the first */
 
 /* Element types of exl3_hadamard_fast. */

@@ -88,8 +88,8 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 WAIT_CAUSES = {
-    _lib.EXL3_WAIT_MOE_FUSED: "a down item of the one-launch one-token MoE layer (EXL3_MOE_FUSED=1) stopped "
-                              "waiting for its h blocks",
+    _lib.EXL3_WAIT_MOE_FUSED: "a down item of a one-launch MoE pass (EXL3_MOE_FUSED=1 or EXL3_MOE_FUSED_ROUTED=1) "
+                              "stopped waiting for its h blocks",
     _lib.EXL3_WAIT_FAT_TAIL: "the second k-half of a wide-tile GEMM tail tile stopped waiting for the first",
 }
 

@@ -2,8 +2,8 @@
 
 Two kernels wait inside a launch: the second k-half of a wide-tile GEMM tail
 tile waits for the first half's partial tile, and a down item of the
-one-launch one-token MoE layer (EXL3_MOE_FUSED=1) waits for the h blocks the
-gate/up items publish.  Both waits are bounded so that every wave exits; a
+one-launch MoE passes (one token, EXL3_MOE_FUSED=1; routed batches,
+EXL3_MOE_FUSED_ROUTED=1) waits for the h blocks the gate/up items publish.  Both waits are bounded so that every wave exits; a
 wait that gives up sets a bit of the workspace status word, which
 exl3_workspace_status / ops.check_waits() report.
 
@@ -101,6 +101,48 @@ def test_moe_fused_wait_that_gives_up_is_reported(monkeypatch):
 
     def run(fused):
         monkeypatch.setenv("EXL3_MOE_FUSED", fused)
+        out = torch.ops.sglang_exl3.exl3_moe_layer(x, ids, w, *tables, K, K, K, cb == 1, inter, 0.0)
+        torch.cuda.synchronize()
+        return out
+
+    two = run("0")
+    ops.check_waits()
+    monkeypatch.setenv("EXL3_WAIT_POLLS", "0")
+    run("1")
+    with pytest.raises(RuntimeError, match="down item"):
+        ops.check_waits()
+    monkeypatch.delenv("EXL3_WAIT_POLLS")
+    again = run("1")
+    ops.check_waits()
+    assert torch.equal(again, two)
+    del keep
+
+
+def test_moe_routed_fused_wait_that_gives_up_is_reported(monkeypatch):
+    """A routed batch in the one-launch gate/up + down pass (EXL3_MOE_FUSED_ROUTED=1): with a
+    zero poll budget the down items stop waiting at once; check_waits() reports it, and the next
+    call matches the separate launches bit for bit."""
+    T, E, hidden, inter, K, cb, topk = 12, 16, 512, 512, 3, 1, 4
+    print(f"case: moe fused routed wait T={T} E={E} h={hidden} i={inter} K={K} topk={topk}", flush=True)
+    monkeypatch.setenv("EXL3_MOE_DN_NSTEPS", "8")  # the fused pass's down items, for both paths
+    rng = np.random.default_rng(530)
+    tabs = {p: ([], [], []) for p in ("gate", "up", "down")}
+    keep = []
+    for e in range(E):
+        for j, (proj, kk, nn) in enumerate((("gate", hidden, inter), ("up", hidden, inter), ("down", inter, hidden))):
+            tr, su, sv = make_weight(kk, nn, K, seed=540 + 3 * e + j)
+            sv = (sv.astype(np.float32) * (4.0 / np.sqrt(kk))).astype(np.float16)
+            dd = [torch.from_numpy(a).cuda() for a in (tr, su, sv)]
+            keep.append(dd)
+            for c, t in zip(tabs[proj], dd):
+                c.append(t.data_ptr())
+    tables = [torch.tensor(c, dtype=torch.int64, device="cuda") for p in ("gate", "up", "down") for c in tabs[p]]
+    x = torch.from_numpy(make_x(T, hidden, seed=531)).cuda()
+    ids = torch.from_numpy(np.stack([rng.choice(E, size=topk, replace=False) for _ in range(T)]).astype(np.int32)).cuda()
+    w = torch.from_numpy((rng.random((T, topk)) + 0.05).astype(np.float32)).cuda()
+
+    def run(fused):
+        monkeypatch.setenv("EXL3_MOE_FUSED_ROUTED", fused)
         out = torch.ops.sglang_exl3.exl3_moe_layer(x, ids, w, *tables, K, K, K, cb == 1, inter, 0.0)
         torch.cuda.synchronize()
         return out
