@@ -865,8 +865,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
 // grid is the device's resident capacity), gate/up items never wait, and a
 // down item waits only for items of lower index, i.e. of its own round or an
 // earlier one, which the other resident workgroups reach without waiting on
-// anything later.  DFX: the down pass adds into the fused combine's
-// fixed-point accumulators (one round trip per split).
+// anything later.  If other work keeps workgroups off the device, a wait
+// gives up and sets EXL3_WAIT_MOE_FUSED in the workspace status word.  DFX:
+// the down pass adds into the fused combine's fixed-point accumulators (one
+// round trip per split).  Opt-in: slower than the separate launches.
 template <int K, int CB, int NSG, int NSD, bool GFX, bool DFX>
 __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_routed_kernel(MoeParams pg, MoeParams pd) {
     extern __shared__ __align__(16) unsigned char mv_smem[];
