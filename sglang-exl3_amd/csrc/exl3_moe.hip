@@ -545,6 +545,10 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     p.partials = reinterpret_cast<float*>(w8 + L.part_off);
     p.direct = direct;
     p.tab_prefetch = env_int("EXL3_MOE_TAB_PREFETCH", 1) != 0;
+    // routed passes pick their column blocks per item from the unit count
+    // (moe_item_bpi); env EXL3_MOE_BPI forces the planner's value, and
+    // EXL3_MOE_BPI_DYN=0 keeps it
+    p.bpi_dyn = env_int("EXL3_MOE_BPI", 0) <= 0 && env_int("EXL3_MOE_BPI_DYN", 1) != 0;
     p.ids = ids;
     p.E = E;
     p.tabs = tb;

@@ -91,6 +91,7 @@ struct MoeParams {
     int splits;        // S
     int kw;            // k waves per workgroup
     int bx_per_item;   // column blocks one item covers (divides n/128)
+    int bpi_dyn;       // routed launches: the kernel sets bx_per_item from the unit count (moe_item_bpi)
     int mode;
     int in_rot;        // GATE_UP: x holds the rows already rotated per projection,
                        // [2][entries][k] by (token, slot) entry (moe_route_rotate_kernel)
@@ -260,12 +261,12 @@ __device__ __forceinline__ void zero_row(__half* out, int n) {
 // 128-wide block of h, and down items wait for the blocks they read.
 template <int K, int CB, int NS, int MODE, int KW, bool FUSED, bool FXS = false, bool GFX = false>
 __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned char* mv_smem, int direct_valid,
-                                         bool first) {
+                                         bool first, int bpi) {
     constexpr int ROWS = MOE_UNIT_ROWS;
     __shared__ int is_last;
     constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
     const int nblk_n = p.n >> 7;
-    const int BPI = p.bx_per_item, ngroups = nblk_n / BPI;
+    const int BPI = bpi, ngroups = nblk_n / BPI;
     const int S = p.splits, P = p.proj_launch;
     const int per_unit = ngroups * P * S;
     const int k = p.k, n = p.n;
@@ -780,6 +781,23 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     }
 }
 
+// Column blocks per item of a routed pass, from the routed unit count: one
+// while the pass has at most 2.75 rounds of the grid in one-block items,
+// otherwise the planner's choice, at least two.  The planner sizes items from
+// the unit count of uniform routing; a skewed router activates far fewer
+// experts (config 4, Zipf 1.1, B = 32: 45 units against 113), and the best
+// choice follows the actual count (graph-timed, one block against two per
+// gate/up item: Zipf B = 16 / 32 / 40 / 64: 45.5 / 54.6 / 64.3 / 89.1 against
+// 49.6 / 58.6 / 65.7 / 81.6 us; uniform B = 8 / 16: 51.3 / 74.5 against 57.7 /
+// 72.6 us).  Outputs do not depend on it: each block's product is the same.
+__device__ __forceinline__ int moe_item_bpi(const MoeParams& p, int nunits, int grid) {
+    const int nblk = p.n >> 7;
+    if (!p.bpi_dyn) return p.bx_per_item;
+    const long long items1 = (long long)nunits * nblk * p.proj_launch * p.splits;
+    if (4 * items1 <= 11LL * grid) return 1;
+    return (p.bx_per_item == 1 && nblk % 2 == 0) ? 2 : p.bx_per_item;
+}
+
 // Persistent over the work items of one projection pass: the grid is sized
 // to the device, the item count comes from the routing kernel (or the slots
 // of a directly routed token), so no workgroup is launched for an inactive
@@ -793,7 +811,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
     constexpr bool down = MODE == MV_DOWN || MODE == MV_DOWN_DIRECT;
     const int nunits = direct ? p.topk : uniform_i(gptr(p.rt.counts)[1]);
-    const int per_unit = ((p.n >> 7) / p.bx_per_item) * p.proj_launch * p.splits;
+    const int bpi = direct ? p.bx_per_item : moe_item_bpi(p, nunits, (int)gridDim.x);
+    const int per_unit = ((p.n >> 7) / bpi) * p.proj_launch * p.splits;
     const int total = nunits * per_unit;
     if ((int)blockIdx.x >= total) return;
     // one token routed directly: its valid slots (the fused combine's count);
@@ -808,7 +827,7 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     }
     const int G = gridDim.x, b0 = blockIdx.x;
     for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0))
-        moe_item<K, CB, NS, MODE, KW, false, FXS, GFX>(p, it, mv_smem, direct_valid, rnd == 0);
+        moe_item<K, CB, NS, MODE, KW, false, FXS, GFX>(p, it, mv_smem, direct_valid, rnd == 0, bpi);
 }
 
 // One token routed directly, gate/up and down in one persistent launch.
@@ -839,8 +858,10 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_direct_kernel(Moe
     const int total = ngu + pd.topk * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
     const int G = gridDim.x;
     for (int rnd = 0, it = blockIdx.x; it < total; ++rnd) {
-        if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true, GFX, GFX>(pg, it, mv_smem, direct_valid, rnd == 0);
-        else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true, GFX, GFX>(pd, it - ngu, mv_smem, direct_valid, rnd == 0);
+        if (it < ngu) moe_item<K, CB, NSG, MV_GU_DIRECT, 1, true, GFX, GFX>(pg, it, mv_smem, direct_valid, rnd == 0,
+                                                                   pg.bx_per_item);
+        else moe_item<K, CB, NSD, MV_DOWN_DIRECT, 1, true, GFX, GFX>(pd, it - ngu, mv_smem, direct_valid, rnd == 0,
+                                                                     pd.bx_per_item);
         if (G >= total) break;
         __syncthreads();
         if (threadIdx.x == 0)
@@ -878,8 +899,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_fused_routed_kernel(Moe
     const int total = ngu + nunits * ((pd.n >> 7) / pd.bx_per_item) * pd.splits;
     const int G = gridDim.x, b0 = blockIdx.x;
     for (int rnd = 0, it = b0; it < total; ++rnd, it = rnd * G + ((rnd & 1) ? G - 1 - b0 : b0)) {
-        if (it < ngu) moe_item<K, CB, NSG, MV_GU_ROT, 1, true, GFX, GFX>(pg, it, mv_smem, 0, rnd == 0);
-        else moe_item<K, CB, NSD, MV_DOWN, 1, true, DFX, GFX>(pd, it - ngu, mv_smem, 0, rnd == 0);
+        if (it < ngu) moe_item<K, CB, NSG, MV_GU_ROT, 1, true, GFX, GFX>(pg, it, mv_smem, 0, rnd == 0, pg.bx_per_item);
+        else moe_item<K, CB, NSD, MV_DOWN, 1, true, DFX, GFX>(pd, it - ngu, mv_smem, 0, rnd == 0, pd.bx_per_item);
     }
 }
 
