@@ -781,21 +781,39 @@ __device__ __forceinline__ void moe_item(const MoeParams& p, int it, unsigned ch
     }
 }
 
-// Column blocks per item of a routed pass, from the routed unit count: one
-// while the pass has at most 2.75 rounds of the grid in one-block items,
-// otherwise the planner's choice, at least two.  The planner sizes items from
-// the unit count of uniform routing; a skewed router activates far fewer
-// experts (config 4, Zipf 1.1, B = 32: 45 units against 113), and the best
-// choice follows the actual count (graph-timed, one block against two per
-// gate/up item: Zipf B = 16 / 32 / 40 / 64: 45.5 / 54.6 / 64.3 / 89.1 against
-// 49.6 / 58.6 / 65.7 / 81.6 us; uniform B = 8 / 16: 51.3 / 74.5 against 57.7 /
-// 72.6 us).  Outputs do not depend on it: each block's product is the same.
+// Column blocks per item of a routed pass, from the routed unit count: the
+// divisor d <= 4 of the pass's column blocks whose item count lands nearest
+// 2.2 rounds of the grid (ties: the smaller d).  The planner sizes items from the
+// unit count of uniform routing; a skewed router activates far fewer experts
+// (config 4, Zipf 1.1, B = 32: 45 units against 113), and the best grouping
+// follows the actual count.  Graph-timed, rounds of the grid -> us: config 4
+// Zipf B = 32: 2.1 / 1.06 -> 54.5 / 58.5 (d = 1 / 2); B = 56: 3.0 / 1.5 -> 81.5 /
+// 77.7; B = 64: 3.3 / 1.66 / 1.1 -> 89.1 / 81.6 / 88.5 (d = 1 / 2 / 3);
+// uniform B = 8: 2.5 / 1.2 -> 51.3 / 57.6; B = 16: 3.8 / 1.9 -> 74.3 / 72.7;
+// config 5 gate/up (K = 2): 6.2 / 3.1 / 2.1 / 1.5 -> 102.9 / 104.2 / 100.3 /
+// 106.9 (d = 1 / 2 / 3 / 4).  Outputs do not depend on it: each block's
+// product is the same.
 __device__ __forceinline__ int moe_item_bpi(const MoeParams& p, int nunits, int grid) {
-    const int nblk = p.n >> 7;
     if (!p.bpi_dyn) return p.bx_per_item;
-    const long long items1 = (long long)nunits * nblk * p.proj_launch * p.splits;
-    if (4 * items1 <= 11LL * grid) return 1;
-    return (p.bx_per_item == 1 && nblk % 2 == 0) ? 2 : p.bx_per_item;
+    const int nblk = p.n >> 7;
+    const int per_block = nunits * p.proj_launch * p.splits;
+    const int target = 11 * grid;  // 5 x items against 11 x grid: 2.2 rounds
+    // candidates d = 1..4 (the divisors that occur at these shapes), the
+    // divisions by constants
+    int best = 1, best_dev = abs(5 * per_block * nblk - target);
+    if (nblk % 2 == 0) {
+        const int dev = abs(5 * per_block * (nblk / 2) - target);
+        if (dev < best_dev) best = 2, best_dev = dev;
+    }
+    if (nblk % 3 == 0) {
+        const int dev = abs(5 * per_block * (nblk / 3) - target);
+        if (dev < best_dev) best = 3, best_dev = dev;
+    }
+    if (nblk % 4 == 0) {
+        const int dev = abs(5 * per_block * (nblk / 4) - target);
+        if (dev < best_dev) best = 4, best_dev = dev;
+    }
+    return best;
 }
 
 // Persistent over the work items of one projection pass: the grid is sized
@@ -811,7 +829,8 @@ __global__ __launch_bounds__(GV_MAX_THREADS, 4) void moe_gemv_kernel(MoeParams p
     constexpr bool direct = MODE == MV_GU_DIRECT || MODE == MV_DOWN_DIRECT;
     constexpr bool down = MODE == MV_DOWN || MODE == MV_DOWN_DIRECT;
     const int nunits = direct ? p.topk : uniform_i(gptr(p.rt.counts)[1]);
-    const int bpi = direct ? p.bx_per_item : moe_item_bpi(p, nunits, (int)gridDim.x);
+    // wave-uniform, in a scalar register (the item decomposition divides by it)
+    const int bpi = direct ? p.bx_per_item : uniform_i(moe_item_bpi(p, nunits, (int)gridDim.x));
     const int per_unit = ((p.n >> 7) / bpi) * p.proj_launch * p.splits;
     const int total = nunits * per_unit;
     if ((int)blockIdx.x >= total) return;
