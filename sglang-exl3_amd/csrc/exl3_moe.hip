@@ -361,7 +361,7 @@ double expected_active(int tokens, int topk, int E) {
 //  * column blocks per item grouped only when the items would exceed
 //    8 x 512 (a few per workgroup of the persistent grid).
 // Env overrides (tuning): EXL3_MOE_NSTEPS, EXL3_MOE_KW, EXL3_MOE_BPI.
-MoePlan plan_moe(double units, int entries, int k, int n, int nproj, double items12) {
+MoePlan plan_moe(double units, int entries, int k, int n, int nproj, double items12, bool fc_pass = false) {
     (void)entries;
     const int kslices = k / 16, nblk = n / 128;
     const double grid = 512.0;
@@ -377,8 +377,15 @@ MoePlan plan_moe(double units, int entries, int k, int n, int nproj, double item
     // 12 / 16 with 744 / 816 / 1097 / 1318 items: 34.7 / 37.4 / 41.9 / 45.2 ->
     // 33.4 / 35.2 / 38.4 / 42.2 us; B = 2 / 4 / 6 with 224 / 466 / 657 items:
     // 22.3 / 27.1 / 29.4 -> 24.2 / 28.9 / 30.7 us).
+    // With the fused combine (fc_pass) only where they leave one split
+    // (k = 768): with two or more the 8-step items win (config 5 down pass,
+    // k = 1536: 12 steps and the adds' LDS tile hold two workgroups per CU, 8
+    // steps three; K = 2 / 3 / 4 / 5: 101.0 / 110.1 / 108.8 / 123.1 -> 98.8 /
+    // 105.8 / 106.5 / 121.3 us).
     int ns = env_int(nproj == 1 ? "EXL3_MOE_DN_NSTEPS" : "EXL3_MOE_GU_NSTEPS", 0);
-    if (ns == 0 && kw == 1 && kslices % 48 == 0 && units * nblk * (kslices / 48) >= items12) ns = 12;
+    if (ns == 0 && kw == 1 && kslices % 48 == 0 && (!fc_pass || kslices == 48) &&
+        units * nblk * (kslices / 48) >= items12)
+        ns = 12;
     if (ns == 12 && kslices % (4 * ns * kw) == 0 && moe_smem_bytes(4 * ns * kw, kw) <= kMaxLds / 2 - 1024)
         return MoePlan{ns, kw, kslices / (4 * ns * kw), 1};
     if (ns <= 0 || ns == 12) ns = env_int("EXL3_MOE_NSTEPS", 8);
@@ -449,7 +456,7 @@ MoeLayout moe_layout(int tokens, int topk, int E, int hidden, int inter) {
     // larger of the two passes') at two workgroups per CU
     L.fr = tokens > 1 && env_int("EXL3_MOE_FUSED_ROUTED", 0) != 0;
     L.gu = plan_moe(units, L.entries, hidden, inter, 2, 1536.0);
-    L.dn = plan_moe(units, L.entries, inter, hidden, 1, L.fr ? 1e30 : (L.fc ? 700.0 : 1536.0));
+    L.dn = plan_moe(units, L.entries, inter, hidden, 1, L.fr ? 1e30 : (L.fc ? 700.0 : 1536.0), L.fc);
     size_t o = kWsScratchOffset;
     L.route_off = o;
     o = align256(o + 4 * sizeof(int));
