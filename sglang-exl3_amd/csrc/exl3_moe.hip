@@ -594,7 +594,15 @@ int run_moe_decode(const char* fn, const uint16_t* x, const int32_t* ids, const 
     // then rotates up to 16 SwiGLU rows per k block, and the adds contend).
     const int gu_kslices = hidden / 16;
     const int gfx_ns = env_int("EXL3_MOE_GFX_GU_NSTEPS", direct ? (fuse_req ? 8 : 4) : L.gu.ns);
-    const bool gfx = (direct || (L.rot && tokens <= env_int("EXL3_MOE_GFX_TOKENS", kMoeGfxTokens))) &&
+    // With 8 or more gate/up splits the partial-row hand-off's last arrival
+    // reads 2 S >= 16 partial rows per element, and the split fixed-point
+    // pass pays one token further (config 5, 4 tokens, 8 splits, K = 2 / 3 /
+    // 4 / 5: 99.0 / 106.2 / 107.8 / 121.8 -> 95.4 / 100.3 / 101.3 / 117.2 us;
+    // config 4, 4 splits, Zipf router, B = 4 / 5 / 6: 27.4 / 30.0 / 29.1 ->
+    // 29.2 / 30.8 / 31.1 us with it).
+    const int gfx_tokens = env_int("EXL3_MOE_GFX_TOKENS", kMoeGfxTokens +
+                                                          (gu_kslices % (4 * gfx_ns) == 0 && gu_kslices / (4 * gfx_ns) >= 8));
+    const bool gfx = (direct || (L.rot && tokens <= gfx_tokens)) &&
                      dn_fxs && moe_gfx_steps_ok(gfx_ns) && moe_gfx_steps_ok(L.dn.ns) &&
                      gu_kslices % (4 * gfx_ns) == 0 && gu_kslices / (4 * gfx_ns) <= SK_MAX_CONTRIB &&
                      ((size_t)tokens * hidden + (size_t)2 * L.entries * inter) * 8 <= kWsAccBytes &&
