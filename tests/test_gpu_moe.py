@@ -711,3 +711,29 @@ def test_moe_prefill_and_decode_paths_agree(monkeypatch):
     ref = ex.ref(x, ids, w)
     check_close(outs["0"], ref, "decode path")
     check_close(outs["1"], ref, "prefill path")
+
+
+@pytest.mark.parametrize("T,E,hidden,inter,K,cb", [
+    (16, 128, 2048, 768, 3, 1),    # uniform routing: the device groups 2 column blocks, the planner 1
+    (4, 64, 4096, 1536, 2, 2),     # 8 gate/up splits: split fixed-point gate/up at 4 tokens, 4-block groups
+])
+def test_moe_column_grouping_keeps_bits(T, E, hidden, inter, K, cb, monkeypatch):
+    """The column blocks per item of a routed pass (chosen on the device from the routed unit
+    count, or forced with EXL3_MOE_BPI) only move work between workgroups: every grouping gives the
+    same bits, and the result matches the oracle."""
+    print(f"case: moe column grouping T={T} E={E} h={hidden} i={inter} K={K} cb={cb}", flush=True)
+    ex = Experts(E, hidden, inter, (K, K, K), cb, seed=250 + T)
+    x = make_x(T, hidden, seed=251 + T)
+    ids, w = _routing(T, 8, E, seed=252 + T)
+    outs = []
+    for dyn, bpi in (("1", None), ("0", None), ("0", "2"), ("0", "3")):
+        monkeypatch.setenv("EXL3_MOE_BPI_DYN", dyn)
+        if bpi is None:
+            monkeypatch.delenv("EXL3_MOE_BPI", raising=False)
+        else:
+            monkeypatch.setenv("EXL3_MOE_BPI", bpi)
+        outs.append(_layer_capi(ex, x, ids, w, cb=cb))
+        torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0]), "column grouping changed the result"
+    check_close(outs[0].float().cpu().numpy(), ex.ref(x, ids, w), f"moe column grouping T={T}")
