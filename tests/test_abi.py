@@ -140,6 +140,26 @@ def test_moe_plan_and_workspace_are_host_only():
     assert L.exl3_moe_workspace_size(0, 8, 128, 2048, 768) == 0
 
 
+def test_moe_plan_down_item_length(monkeypatch):
+    """Down items of 12 steps (48 k-slices) where they leave one split with the fused combine
+    (config 4, k = 768), 8-step items where 12 would leave two (config 5, k = 1536, 4 tokens);
+    without the fused combine (above 48 tokens) 12 steps also with two splits."""
+    for name in ("EXL3_MOE_DN_NSTEPS", "EXL3_MOE_NSTEPS", "EXL3_MOE_FC_TOKENS", "EXL3_MOE_FUSED_ROUTED"):
+        monkeypatch.delenv(name, raising=False)
+    L = _lib.lib()
+    out = (ctypes.c_int * 9)()
+
+    def down(T, topk, E, hidden, inter):
+        assert L.exl3_moe_plan(T, topk, E, hidden, inter, out) == 0
+        return out[5], out[7]  # steps, splits
+
+    assert down(16, 8, 128, 2048, 768) == (12, 1)     # config 4, fused combine, one split
+    assert down(4, 9, 289, 4096, 1536) == (8, 3)      # config 5: 8-step items, three splits
+    assert down(64, 9, 289, 4096, 1536) == (12, 2)    # separate combine: two splits of 12 steps
+    monkeypatch.setenv("EXL3_MOE_DN_NSTEPS", "12")    # the override still forces 12 steps
+    assert down(4, 9, 289, 4096, 1536) == (12, 2)
+
+
 def test_moe_rejects_bad_arguments_without_a_gpu():
     L = _lib.lib()
     nul = [None] * 9
